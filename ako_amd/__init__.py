@@ -1,0 +1,23 @@
+"""AKO's candidate kernels, MI355X-native.
+
+Public operations keep the signatures of Farx1/AKO's ``ako`` package
+(``ako/__init__.py:5-17``); kernel choice goes through the same gated,
+benchmark-driven selector, and the gfx950 HIP kernels race the PyTorch
+baselines as ``backend="hip"`` candidates.
+"""
+
+__version__ = "0.1.0"
+
+from ako_amd.ops.rmsnorm import rmsnorm, rmsnorm_residual
+from ako_amd.ops.rope import build_rope_tables, rope, rope_qk
+from ako_amd.ops.swiglu import swiglu
+
+__all__ = [
+    "__version__",
+    "build_rope_tables",
+    "rmsnorm",
+    "rmsnorm_residual",
+    "rope",
+    "rope_qk",
+    "swiglu",
+]

@@ -1,0 +1,153 @@
+"""ctypes binding of ``libako_hip.so`` (declared in ``include/ako_hip.h``).
+
+Loading is lazy and happens once. It fails loudly: a missing or mismatched
+library raises ``HipLibraryError`` rather than letting any caller fall back
+to a CPU or PyTorch path. Two checks run at load time:
+
+* the ABI version compiled into the library equals ``ABI_VERSION``;
+* the HIP runtime the library is bound to is the one PyTorch uses
+  (``hipRuntimeGetVersion`` against ``torch.version.hip``). The library is
+  linked against torch's bundled ``libamdhip64``; if some other runtime were
+  resolved, device pointers and stream handles from torch would belong to a
+  different runtime instance.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Any
+
+import torch
+
+ABI_VERSION = 1
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libako_hip.so"
+
+AKO_OK = 0
+AKO_ERR_INVALID_ARGUMENT = 1
+AKO_ERR_UNSUPPORTED = 2
+AKO_ERR_HIP = 3
+AKO_ERR_NO_DEVICE = 4
+
+DTYPE_CODES: dict[torch.dtype, int] = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+ROPE_STYLE_CODES = {"neox": 0, "interleaved": 1}
+
+#: Every symbol the header declares, with its (restype, argtypes).
+_i64, _int, _ptr, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+_i64p = ctypes.POINTER(ctypes.c_int64)
+SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
+    "ako_abi_version": (_int, []),
+    "ako_hip_runtime_version": (_int, []),
+    "ako_build_info": (ctypes.c_char_p, []),
+    "ako_last_error": (ctypes.c_char_p, []),
+    "ako_rmsnorm_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _f32, _int, _int, _ptr]),
+    "ako_rmsnorm_residual_fwd": (
+        _int,
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _ptr],
+    ),
+    "ako_rope_fwd": (
+        _int,
+        [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _int, _int, _int, _ptr],
+    ),
+    "ako_rope_qk_fwd": (
+        _int,
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p,
+         _i64p, _i64, _int, _int, _int, _ptr],
+    ),
+    "ako_swiglu_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _int, _ptr]),
+    "ako_set_tuning": (_int, [_int, _int, _int]),
+}
+
+
+class HipLibraryError(RuntimeError):
+    """The HIP kernel library is missing, stale, or bound to the wrong runtime."""
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("AKO_HIP_LIB")
+    return Path(override) if override else LIB_PATH
+
+
+def _expected_runtime_version() -> int | None:
+    """``torch.version.hip`` ("7.0.51831") as hipRuntimeGetVersion encodes it."""
+    text = getattr(torch.version, "hip", None)
+    if not text:
+        return None
+    parts = [int(p) for p in text.split(".")[:3] if p.isdigit()]
+    while len(parts) < 3:
+        parts.append(0)
+    major, minor, patch = parts
+    return major * 10_000_000 + minor * 100_000 + patch
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises ``HipLibraryError`` when it cannot be used."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise HipLibraryError(
+            f"{path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(or `python -m ako_amd._build`) first"
+        )
+    try:
+        lib = ctypes.CDLL(str(path))
+    except OSError as exc:
+        raise HipLibraryError(f"cannot load {path}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            raise HipLibraryError(f"{path} does not export {name}")
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.ako_abi_version() != ABI_VERSION:
+        raise HipLibraryError(
+            f"{path} has ABI {lib.ako_abi_version()}, this package needs {ABI_VERSION}; rebuild it"
+        )
+    expected = _expected_runtime_version()
+    bound = lib.ako_hip_runtime_version()
+    if expected is not None and bound != expected:
+        raise HipLibraryError(
+            f"{path} is bound to HIP runtime {bound}, but torch uses {expected} "
+            f"({torch.version.hip}); the library must link torch's libamdhip64"
+        )
+    _lib = lib
+    return lib
+
+
+def is_available() -> bool:
+    try:
+        load()
+    except HipLibraryError:
+        return False
+    return True
+
+
+def last_error() -> str:
+    raw = load().ako_last_error()
+    return raw.decode() if raw else ""
+
+
+def check(status: int, fn_name: str) -> None:
+    """Turn a nonzero ``ako_status_t`` into the reference's exception types."""
+    if status == AKO_OK:
+        return
+    message = f"{fn_name}: {last_error()}"
+    if status in (AKO_ERR_INVALID_ARGUMENT, AKO_ERR_UNSUPPORTED):
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def set_tuning(op: int, key: int, value: int) -> None:
+    check(load().ako_set_tuning(op, key, value), "ako_set_tuning")
+
+
+def current_stream(device: torch.device) -> int:
+    """Raw ``hipStream_t`` of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,149 @@
+"""HBM roofline accounting for the streaming kernels.
+
+The four operations do O(1) flops per byte, so their bound is HBM bandwidth
+(MFMA is deliberately unused). ``alg_bytes_*`` give the bytes a perfect
+kernel must move per call (every input read once, every output written
+once); achieved bandwidth is that figure over the measured device time.
+
+Device time comes from HIP events recorded on the stream the kernels are
+launched on (the HIP candidates launch on torch's current stream, so
+``torch.cuda.Event`` records land on the same stream). To keep a
+measurement cold without a per-call flush, callers cycle through input sets
+whose total size exceeds twice the MI355X's Infinity Cache (256 MB) plus its
+L2s (``copies_for_cold``), so no launch finds its inputs cached.
+"""
+
+from __future__ import annotations
+
+import statistics
+from dataclasses import dataclass, field
+from typing import Any, Callable, Sequence
+
+import torch
+
+#: Published peak HBM bandwidth per ISA, GB/s (MI355X/MI350X: 8 TB/s HBM3E;
+#: MI300X/MI325X: 5.3/6.0 TB/s; the gfx942 figure is the MI300X one).
+HBM_PEAK_GBPS = {"gfx950": 8000.0, "gfx942": 5300.0}
+#: Infinity Cache (MALL) + aggregate L2 per ISA, bytes: what a cold
+#: measurement must exceed.
+CACHE_BYTES = {"gfx950": 256 * 2**20 + 8 * 4 * 2**20, "gfx942": 256 * 2**20 + 8 * 4 * 2**20}
+
+
+def elem_bytes(dtype: torch.dtype) -> int:
+    return torch.finfo(dtype).bits // 8
+
+
+def alg_bytes_rmsnorm(rows: int, hidden: int, dtype: torch.dtype, w_dtype: torch.dtype | None = None) -> int:
+    b = elem_bytes(dtype)
+    return 2 * rows * hidden * b + hidden * elem_bytes(w_dtype or dtype)
+
+
+def alg_bytes_rmsnorm_residual(rows: int, hidden: int, dtype: torch.dtype,
+                               w_dtype: torch.dtype | None = None) -> int:
+    b = elem_bytes(dtype)
+    return 4 * rows * hidden * b + hidden * elem_bytes(w_dtype or dtype)
+
+
+def alg_bytes_rope(batch: int, seq: int, heads: int, head_dim: int, dtype: torch.dtype,
+                   table_dtype: torch.dtype) -> int:
+    return 2 * batch * seq * heads * head_dim * elem_bytes(dtype) + 2 * seq * (head_dim // 2) * elem_bytes(table_dtype)
+
+
+def alg_bytes_swiglu(rows: int, n: int, dtype: torch.dtype) -> int:
+    return 3 * rows * n * elem_bytes(dtype)
+
+
+def device_arch(device: torch.device | None = None) -> str | None:
+    if not torch.cuda.is_available():
+        return None
+    props = torch.cuda.get_device_properties(device or torch.cuda.current_device())
+    return str(getattr(props, "gcnArchName", "")).split(":")[0] or None
+
+
+def hbm_peak_gbps(device: torch.device | None = None) -> float:
+    """Published peak of this device's ISA (MI355X figure when unknown)."""
+    return HBM_PEAK_GBPS.get(device_arch(device) or "", HBM_PEAK_GBPS["gfx950"])
+
+
+def copies_for_cold(bytes_per_set: int, device: torch.device | None = None, minimum: int = 2) -> int:
+    """Input sets to rotate through so the cycle exceeds twice MALL + L2."""
+    cache = CACHE_BYTES.get(device_arch(device) or "", CACHE_BYTES["gfx950"])
+    need = -(-2 * cache // max(bytes_per_set, 1))
+    return max(minimum, int(need))
+
+
+@dataclass
+class LaunchStats:
+    """Per-launch device durations of one kernel configuration."""
+
+    name: str
+    alg_bytes: int
+    durations_ms: list[float] = field(default_factory=list)
+
+    @property
+    def mean_ms(self) -> float:
+        return statistics.fmean(self.durations_ms) if self.durations_ms else 0.0
+
+    @property
+    def p50_ms(self) -> float:
+        return statistics.median(self.durations_ms) if self.durations_ms else 0.0
+
+    def gbps(self, which: str = "mean") -> float:
+        ms = self.mean_ms if which == "mean" else self.p50_ms
+        return self.alg_bytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+
+    def to_dict(self, peak_gbps: float) -> dict[str, Any]:
+        return {
+            "name": self.name,
+            "alg_bytes": self.alg_bytes,
+            "launches": len(self.durations_ms),
+            "mean_us": round(self.mean_ms * 1e3, 3),
+            "p50_us": round(self.p50_ms * 1e3, 3),
+            "gbps": round(self.gbps(), 1),
+            "pct_hbm_peak": round(100.0 * self.gbps() / peak_gbps, 2),
+        }
+
+
+def time_steps(calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int) -> float:
+    """Milliseconds for ``steps`` back-to-back passes over ``calls``, bracketed by
+    one pair of events (no per-launch events inside, so nothing but the
+    kernels and their launches is timed)."""
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    begin.record(stream)
+    for _ in range(steps):
+        for _, _, fn in calls:
+            fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end)
+
+
+def time_each_launch(
+    calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int
+) -> list[LaunchStats]:
+    """Per-launch device durations: an event pair around every launch of
+    ``steps`` passes over ``calls`` (name, alg_bytes, thunk)."""
+    stream = torch.cuda.current_stream()
+    marks = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in calls] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for step in range(steps):
+        for (_, _, fn), (ev0, ev1) in zip(calls, marks[step]):
+            ev0.record(stream)
+            fn()
+            ev1.record(stream)
+    torch.cuda.synchronize()
+    stats: dict[str, LaunchStats] = {}
+    for step in range(steps):
+        for (name, nbytes, _), (ev0, ev1) in zip(calls, marks[step]):
+            stats.setdefault(name, LaunchStats(name, nbytes)).durations_ms.append(ev0.elapsed_time(ev1))
+    return list(stats.values())
+
+
+def warm(calls: Sequence[tuple[str, int, Callable[[], Any]]], passes: int) -> None:
+    for _ in range(passes):
+        for _, _, fn in calls:
+            fn()
+    torch.cuda.synchronize()

@@ -1,0 +1,335 @@
+// The C ABI (include/ako_hip.h): argument validation, status codes, and the
+// hand-off to the kernel launchers. Validation runs entirely on the host and
+// before any HIP call, so every rejection path is testable on a machine
+// without a GPU.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <limits>
+#include <string>
+
+#include "ako_hip.h"
+#include "launch.h"
+
+#ifndef AKO_RMS_NT
+#define AKO_RMS_NT 1
+#endif
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return AKO_OK;
+  if (err == hipErrorNoDevice || err == hipErrorInvalidDevice)
+    return fail(AKO_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(err));
+  return fail(AKO_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+bool valid_dtype(int dt) { return dt == AKO_DTYPE_F32 || dt == AKO_DTYPE_F16 || dt == AKO_DTYPE_BF16; }
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case AKO_DTYPE_F32: return "f32";
+    case AKO_DTYPE_F16: return "f16";
+    case AKO_DTYPE_BF16: return "bf16";
+    default: return "?";
+  }
+}
+
+bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+// Byte range [lo, hi) spanned by `count` rows of `width` elements, `stride` apart.
+struct Span {
+  uintptr_t lo = 0, hi = 0;
+};
+
+Span span_2d(const void* p, int64_t rows, int64_t width, int64_t stride, int elem) {
+  Span s;
+  s.lo = reinterpret_cast<uintptr_t>(p);
+  const int64_t last = (rows - 1) * stride + width;
+  s.hi = s.lo + static_cast<uintptr_t>(last) * elem;
+  return s;
+}
+
+bool overlap(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
+
+constexpr int64_t kMaxInt = std::numeric_limits<int32_t>::max();
+
+}  // namespace
+
+extern "C" {
+
+int ako_abi_version(void) { return AKO_ABI_VERSION; }
+
+int ako_hip_runtime_version(void) {
+  int v = 0;
+  if (hipRuntimeGetVersion(&v) != hipSuccess) return -1;
+  return v;
+}
+
+const char* ako_build_info(void) {
+  static const std::string info = std::string("ako_hip abi=") + std::to_string(AKO_ABI_VERSION) +
+                                  " arch=gfx950 hip_headers=" + std::to_string(HIP_VERSION) +
+                                  " rms_nontemporal=" + std::to_string(AKO_RMS_NT);
+  return info.c_str();
+}
+
+const char* ako_last_error(void) { return g_last_error.c_str(); }
+
+int ako_set_tuning(int op, int key, int value) {
+  if (value < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "tuning value must be >= 0, got %d", value);
+  switch (op) {
+    case 0:
+      if (key == 1) { ako::g_rms_tuning.waves_per_row = value; return AKO_OK; }
+      if (key == 2) { ako::g_rms_tuning.vecs_per_thread = value; return AKO_OK; }
+      if (key == 3) { ako::g_rms_tuning.force_stream = value; return AKO_OK; }
+      break;
+    case 1:
+      if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }
+      if (key == 2) { ako::g_rope_tuning.iters = value; return AKO_OK; }
+      break;
+    case 2:
+      if (key == 1) { ako::g_swiglu_tuning.vecs_per_thread = value; return AKO_OK; }
+      if (key == 2) { ako::g_swiglu_tuning.block = value; return AKO_OK; }
+      break;
+    default:
+      break;
+  }
+  return fail(AKO_ERR_INVALID_ARGUMENT, "unknown tuning key op=%d key=%d", op, key);
+}
+
+// ---------------------------------------------------------------- RMSNorm --
+static int rmsnorm_common(const void* x, const void* r, const void* w, void* y, void* rout,
+                          int64_t rows, int64_t hidden, int64_t sx, int64_t sr, int64_t sy,
+                          int64_t srout, float eps, int dtype, int w_dtype, void* stream,
+                          bool residual) {
+  const char* fn = residual ? "ako_rmsnorm_residual_fwd" : "ako_rmsnorm_fwd";
+  if (!valid_dtype(dtype)) return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code %d", fn, dtype);
+  if (w_dtype != dtype && w_dtype != AKO_DTYPE_F32)
+    return fail(AKO_ERR_UNSUPPORTED, "%s: weight dtype %s with input dtype %s (weight must match or be f32)",
+                fn, dtype_name(w_dtype), dtype_name(dtype));
+  if (rows < 0 || hidden < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size rows=%lld hidden=%lld", fn, (long long)rows, (long long)hidden);
+  if (rows == 0 || hidden == 0) return AKO_OK;
+  if (hidden > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: hidden=%lld exceeds 2^31-1", fn, (long long)hidden);
+  if (!x || !w || !y || (residual && (!r || !rout)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  if (!(eps >= 0.0f)) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: eps must be >= 0", fn);
+  if (sx < 0 || sy < 0 || (residual && (sr < 0 || srout < 0)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative row stride", fn);
+  if (rows > 1 && (sy < hidden || (residual && srout < hidden)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output row stride smaller than hidden (rows would overlap)", fn);
+  const int eb = ako::dtype_bytes(dtype);
+  const Span sy_span = span_2d(y, rows, hidden, sy, eb);
+  const Span sx_span = span_2d(x, rows, hidden, sx, eb);
+  const Span w_span = span_2d(w, 1, hidden, hidden, ako::dtype_bytes(w_dtype));
+  if (overlap(sy_span, sx_span) || overlap(sy_span, w_span))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output y overlaps an input", fn);
+  if (residual) {
+    const Span sr_span = span_2d(r, rows, hidden, sr, eb);
+    const Span so_span = span_2d(rout, rows, hidden, srout, eb);
+    if (overlap(sy_span, sr_span) || overlap(so_span, sx_span) || overlap(so_span, sr_span) ||
+        overlap(so_span, w_span) || overlap(so_span, sy_span))
+      return fail(AKO_ERR_INVALID_ARGUMENT, "%s: residual_out overlaps another buffer", fn);
+  }
+  bool vec = aligned(x, 16) && aligned(y, 16) && aligned(w, 16) && (sx * eb) % 16 == 0 &&
+             (sy * eb) % 16 == 0;
+  if (residual) vec = vec && aligned(r, 16) && aligned(rout, 16) && (sr * eb) % 16 == 0 && (srout * eb) % 16 == 0;
+  // Rows with a padded stride may be vector-aligned while hidden is not a
+  // multiple of the packet; the kernel handles that tail with scalar lanes.
+  ako::RmsArgs a{x, r, w, y, rout, rows, hidden, sx, sr, sy, srout, eps, dtype, w_dtype, residual, vec};
+  return hip_status(ako::launch_rmsnorm(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int ako_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
+                    int64_t x_row_stride, int64_t y_row_stride, float eps, int dtype, int w_dtype,
+                    void* stream) {
+  return rmsnorm_common(x, nullptr, w, y, nullptr, rows, hidden, x_row_stride, 0, y_row_stride, 0,
+                        eps, dtype, w_dtype, stream, false);
+}
+
+int ako_rmsnorm_residual_fwd(const void* x, const void* residual, const void* w, void* y,
+                             void* residual_out, int64_t rows, int64_t hidden,
+                             int64_t x_row_stride, int64_t r_row_stride, int64_t y_row_stride,
+                             int64_t rout_row_stride, float eps, int dtype, int w_dtype,
+                             void* stream) {
+  return rmsnorm_common(x, residual, w, y, residual_out, rows, hidden, x_row_stride, r_row_stride,
+                        y_row_stride, rout_row_stride, eps, dtype, w_dtype, stream, true);
+}
+
+// ------------------------------------------------------------------- RoPE --
+namespace {
+
+struct RopeTensorIn {
+  const void* x;
+  void* y;
+  int64_t heads;
+  const int64_t* xs;  // strides b, s, h
+  const int64_t* ys;
+};
+
+// Extent, in elements, of a [batch, seq, heads, head_dim] view with the given
+// strides (last dimension contiguous): offset of the last element + 1.
+int64_t extent4(int64_t b, int64_t s, int64_t h, int64_t d, const int64_t* st) {
+  return (b - 1) * st[0] + (s - 1) * st[1] + (h - 1) * st[2] + d;
+}
+
+int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos, const void* sin,
+                int64_t batch, int64_t seq, int64_t head_dim, int64_t st, int dtype,
+                int table_dtype, int style, void* stream) {
+  if (!valid_dtype(dtype) || !valid_dtype(table_dtype))
+    return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code (x %d, table %d)", fn, dtype, table_dtype);
+  if (style != AKO_ROPE_NEOX && style != AKO_ROPE_INTERLEAVED)
+    return fail(AKO_ERR_UNSUPPORTED, "%s: unknown RoPE style %d", fn, style);
+  if (batch < 0 || seq < 0 || head_dim < 0)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  if (head_dim % 2 != 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: head_dim must be even, got %lld", fn, (long long)head_dim);
+  int64_t total_heads = 0;
+  for (int i = 0; i < nt; ++i) {
+    if (ts[i].heads < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative head count", fn);
+    total_heads += ts[i].heads;
+  }
+  if (batch == 0 || seq == 0 || head_dim == 0 || total_heads == 0) return AKO_OK;
+  if (head_dim > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: head_dim too large", fn);
+  if (!cos || !sin) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null table pointer", fn);
+  if (st < head_dim / 2 && seq > 1) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: table row stride %lld < head_dim/2", fn, (long long)st);
+  const int eb = ako::dtype_bytes(dtype);
+  const int tb = ako::dtype_bytes(table_dtype);
+  const Span cos_span = span_2d(cos, seq, head_dim / 2, st, tb);
+  const Span sin_span = span_2d(sin, seq, head_dim / 2, st, tb);
+  Span out_spans[2], in_spans[2];
+  for (int i = 0; i < nt; ++i) {
+    const RopeTensorIn& t = ts[i];
+    if (t.heads == 0) continue;
+    if (!t.x || !t.y || !t.xs || !t.ys) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
+    for (int k = 0; k < 3; ++k)
+      if (t.xs[k] < 0 || t.ys[k] < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative stride", fn);
+    // Distinct output elements must not alias: require the usual nesting.
+    if ((t.heads > 1 && t.ys[2] < head_dim) || (seq > 1 && t.ys[1] < t.heads * head_dim) ||
+        (batch > 1 && t.ys[0] < seq * t.heads * head_dim))
+      return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output strides make rows overlap", fn);
+    in_spans[i] = Span{reinterpret_cast<uintptr_t>(t.x),
+                       reinterpret_cast<uintptr_t>(t.x) + static_cast<uintptr_t>(extent4(batch, seq, t.heads, head_dim, t.xs)) * eb};
+    out_spans[i] = Span{reinterpret_cast<uintptr_t>(t.y),
+                        reinterpret_cast<uintptr_t>(t.y) + static_cast<uintptr_t>(extent4(batch, seq, t.heads, head_dim, t.ys)) * eb};
+  }
+  for (int i = 0; i < nt; ++i) {
+    if (ts[i].heads == 0) continue;
+    if (overlap(out_spans[i], cos_span) || overlap(out_spans[i], sin_span))
+      return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output overlaps a table", fn);
+    for (int k = 0; k < nt; ++k) {
+      if (ts[k].heads == 0) continue;
+      if (overlap(out_spans[i], in_spans[k]))
+        return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output overlaps an input", fn);
+      if (k != i && overlap(out_spans[i], out_spans[k]))
+        return fail(AKO_ERR_INVALID_ARGUMENT, "%s: the two outputs overlap", fn);
+    }
+  }
+
+  const bool neox = style == AKO_ROPE_NEOX;
+  const int64_t E = 16 / eb;
+  const int64_t unit = neox ? head_dim / 2 : head_dim;
+  const int64_t table_vals = neox ? E : E / 2;  // table values one lane loads
+  const int64_t tab_align = std::min<int64_t>(16, table_vals * tb);
+  bool vec = unit % E == 0 && unit / E <= 64 && aligned(cos, tab_align) && aligned(sin, tab_align) &&
+             (st * tb) % tab_align == 0;
+  for (int i = 0; i < nt && vec; ++i) {
+    const RopeTensorIn& t = ts[i];
+    if (t.heads == 0) continue;
+    vec = aligned(t.x, 16) && aligned(t.y, 16);
+    for (int k = 0; k < 3 && vec; ++k) vec = t.xs[k] % E == 0 && t.ys[k] % E == 0;
+  }
+
+  ako::RopeArgs a{};
+  const ako::RopeTensorArgs none{nullptr, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  auto conv = [&](const RopeTensorIn& t) {
+    if (t.heads == 0) return none;
+    return ako::RopeTensorArgs{t.x, t.y, t.heads, t.xs[0], t.xs[1], t.xs[2], t.ys[0], t.ys[1], t.ys[2]};
+  };
+  a.t0 = conv(ts[0]);
+  a.t1 = nt > 1 ? conv(ts[1]) : none;
+  if (a.t0.heads == 0) { a.t0 = a.t1; a.t1 = none; }
+  a.cos = cos;
+  a.sin = sin;
+  a.batch = batch;
+  a.seq = seq;
+  a.head_dim = head_dim;
+  a.st = st;
+  a.dtype = dtype;
+  a.table_dtype = table_dtype;
+  a.neox = neox;
+  a.vector_ok = vec;
+  return hip_status(ako::launch_rope(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // namespace
+
+int ako_rope_fwd(const void* x, const void* cos_table, const void* sin_table, void* y,
+                 int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int64_t x_stride_b,
+                 int64_t x_stride_s, int64_t x_stride_h, int64_t y_stride_b, int64_t y_stride_s,
+                 int64_t y_stride_h, int64_t table_row_stride, int dtype, int table_dtype,
+                 int style, void* stream) {
+  const int64_t xs[3] = {x_stride_b, x_stride_s, x_stride_h};
+  const int64_t ys[3] = {y_stride_b, y_stride_s, y_stride_h};
+  const RopeTensorIn t{x, y, heads, xs, ys};
+  return rope_common("ako_rope_fwd", &t, 1, cos_table, sin_table, batch, seq, head_dim,
+                     table_row_stride, dtype, table_dtype, style, stream);
+}
+
+int ako_rope_qk_fwd(const void* q, const void* k, const void* cos_table, const void* sin_table,
+                    void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t q_heads,
+                    int64_t k_heads, int64_t head_dim, const int64_t* q_strides,
+                    const int64_t* k_strides, const int64_t* q_out_strides,
+                    const int64_t* k_out_strides, int64_t table_row_stride, int dtype,
+                    int table_dtype, int style, void* stream) {
+  const RopeTensorIn ts[2] = {{q, q_out, q_heads, q_strides, q_out_strides},
+                              {k, k_out, k_heads, k_strides, k_out_strides}};
+  return rope_common("ako_rope_qk_fwd", ts, 2, cos_table, sin_table, batch, seq, head_dim,
+                     table_row_stride, dtype, table_dtype, style, stream);
+}
+
+// ----------------------------------------------------------------- SwiGLU --
+int ako_swiglu_fwd(const void* gate, const void* up, void* y, int64_t rows, int64_t n,
+                   int64_t gate_row_stride, int64_t up_row_stride, int64_t y_row_stride,
+                   int dtype, void* stream) {
+  const char* fn = "ako_swiglu_fwd";
+  if (!valid_dtype(dtype)) return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code %d", fn, dtype);
+  if (rows < 0 || n < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  if (rows == 0 || n == 0) return AKO_OK;
+  if (n > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: n=%lld exceeds 2^31-1", fn, (long long)n);
+  if (!gate || !up || !y) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  if (gate_row_stride < 0 || up_row_stride < 0 || y_row_stride < 0)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative row stride", fn);
+  if (rows > 1 && y_row_stride < n)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output row stride smaller than n (rows would overlap)", fn);
+  const int eb = ako::dtype_bytes(dtype);
+  const Span ys = span_2d(y, rows, n, y_row_stride, eb);
+  if (overlap(ys, span_2d(gate, rows, n, gate_row_stride, eb)) ||
+      overlap(ys, span_2d(up, rows, n, up_row_stride, eb)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output overlaps an input", fn);
+  const bool contiguous = rows == 1 || (gate_row_stride == n && up_row_stride == n && y_row_stride == n);
+  const bool vec = aligned(gate, 16) && aligned(up, 16) && aligned(y, 16) &&
+                   (contiguous || ((gate_row_stride * eb) % 16 == 0 && (up_row_stride * eb) % 16 == 0 &&
+                                   (y_row_stride * eb) % 16 == 0));
+  ako::SwigluArgs a{gate, up, y, rows, n, gate_row_stride, up_row_stride, y_row_stride, dtype,
+                    contiguous, vec};
+  return hip_status(ako::launch_swiglu(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // extern "C"

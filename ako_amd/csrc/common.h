@@ -1,0 +1,117 @@
+// Shared device helpers for the gfx950 (CDNA4) streaming kernels.
+//
+// Storage types are float, _Float16 and __bf16. Every kernel widens to fp32,
+// computes, and narrows with round-to-nearest-even (v_cvt_f16_f32 and, on
+// gfx950, v_cvt_pk_bf16_f32). Global memory is moved in 16-byte packets
+// (global_load_dwordx4 / global_store_dwordx4), optionally with the
+// non-temporal hint for data that is touched exactly once.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ako {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- scalar conversions -------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
+  return static_cast<_Float16>(v);
+}
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
+  return static_cast<__bf16>(v);
+}
+
+// ---- raw packets of 2..16 bytes --------------------------------------------
+template <int BYTES> struct RawOf;
+template <> struct RawOf<16> { using type = u32x4; };
+template <> struct RawOf<8> { using type = u32x2; };
+template <> struct RawOf<4> { using type = unsigned int; };
+template <> struct RawOf<2> { using type = unsigned short; };
+
+// N elements of T viewed as one register packet (N * sizeof(T) <= 16 bytes).
+template <typename T, int N>
+union Pack {
+  static constexpr int kBytes = N * static_cast<int>(sizeof(T));
+  using raw_t = typename RawOf<kBytes>::type;
+  raw_t raw;
+  T e[N];
+};
+
+template <bool NT, typename R>
+__device__ __forceinline__ R load_raw(const R* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
+template <bool NT, typename R>
+__device__ __forceinline__ void store_raw(R* p, R v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
+
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ Pack<T, N> load_pack(const T* p) {
+  Pack<T, N> pk;
+  pk.raw = load_raw<NT>(reinterpret_cast<const typename Pack<T, N>::raw_t*>(p));
+  return pk;
+}
+
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void store_pack(T* p, const Pack<T, N>& pk) {
+  store_raw<NT>(reinterpret_cast<typename Pack<T, N>::raw_t*>(p), pk.raw);
+}
+
+// N consecutive elements of T (any N that splits into <=16-byte packets),
+// widened to fp32. p must be aligned to min(16, N * sizeof(T)) bytes.
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void load_f32(const T* p, float (&out)[N]) {
+  constexpr int kPer = (16 / static_cast<int>(sizeof(T))) < N ? (16 / static_cast<int>(sizeof(T))) : N;
+  static_assert(N % kPer == 0, "pack split");
+#pragma unroll
+  for (int c = 0; c < N / kPer; ++c) {
+    Pack<T, kPer> pk = load_pack<T, kPer, NT>(p + c * kPer);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) out[c * kPer + i] = to_f32(pk.e[i]);
+  }
+}
+
+// ---- wavefront reduction ----------------------------------------------------
+// Butterfly all-reduce over 64 lanes: DPP quad permutes and row mirrors inside
+// each 16-lane row (no LDS traffic), then two ds_bpermute steps across rows.
+// Every step adds a lane to its partner symmetrically, so all 64 lanes end
+// with the bitwise-identical total.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of each 8 lanes
+  v += dpp_mov<0x140>(v);  // row_mirror: the other half of each 16-lane row
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ako

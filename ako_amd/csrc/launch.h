@@ -1,0 +1,83 @@
+// Internal launcher interface between the C ABI layer (abi.hip) and the
+// kernel translation units. Arguments reaching these functions have already
+// been validated by abi.hip: sizes positive, pointers non-null and aligned as
+// the chosen path requires, strides consistent.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ako {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+inline int dtype_bytes(int dt) { return dt == kF32 ? 4 : 2; }
+
+// Launch-shape overrides set through ako_set_tuning (0 = heuristic).
+struct RmsTuning {
+  int waves_per_row = 0;    // key 1
+  int vecs_per_thread = 0;  // key 2
+  int force_stream = 0;     // key 3: 1 = always use the two-pass kernel
+};
+struct RopeTuning {
+  int tokens_per_block = 0;  // key 1: waves (one token each) per workgroup
+  int iters = 0;             // key 2: head chunks unrolled per loop trip
+};
+struct SwigluTuning {
+  int vecs_per_thread = 0;  // key 1
+  int block = 0;            // key 2: threads per workgroup (64..1024)
+};
+extern RmsTuning g_rms_tuning;
+extern RopeTuning g_rope_tuning;
+extern SwigluTuning g_swiglu_tuning;
+
+struct RmsArgs {
+  const void* x;
+  const void* r;  // residual input (residual variant only)
+  const void* w;
+  void* y;
+  void* rout;     // residual output (residual variant only)
+  int64_t rows;
+  int64_t hidden;
+  int64_t sx, sr, sy, srout;  // row strides, elements
+  float eps;
+  int dtype;
+  int w_dtype;
+  bool residual;
+  bool vector_ok;  // 16-byte packets are aligned for every row
+};
+hipError_t launch_rmsnorm(const RmsArgs& a, hipStream_t stream);
+
+struct RopeTensorArgs {
+  const void* x;
+  void* y;
+  int64_t heads;
+  int64_t sxb, sxs, sxh;
+  int64_t syb, sys, syh;
+};
+struct RopeArgs {
+  RopeTensorArgs t0;
+  RopeTensorArgs t1;  // heads == 0 when only one tensor is rotated
+  const void* cos;
+  const void* sin;
+  int64_t batch, seq, head_dim;
+  int64_t st;  // table row stride, elements
+  int dtype, table_dtype;
+  bool neox;
+  bool vector_ok;
+};
+hipError_t launch_rope(const RopeArgs& a, hipStream_t stream);
+
+struct SwigluArgs {
+  const void* g;
+  const void* u;
+  void* y;
+  int64_t rows, n;
+  int64_t sg, su, sy;
+  int dtype;
+  bool contiguous;  // all three are one dense [rows * n] block
+  bool vector_ok;
+};
+hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t stream);
+
+}  // namespace ako

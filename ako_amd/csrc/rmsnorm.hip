@@ -1,0 +1,317 @@
+// RMSNorm and residual-add + RMSNorm for gfx950.
+//
+// Two kernels:
+//
+// rmsnorm_reg  - the row lives in registers. A row is owned by WPR wavefronts
+//   (64 * WPR lanes); lane t of the row holds the 16-byte packets
+//   t, t + 64*WPR, t + 2*64*WPR, ... (VPT of them), so every wavefront-wide
+//   load instruction covers 1 KiB of contiguous memory. HBM is touched once
+//   per element: x (and the residual) are read once, y (and the new
+//   residual) written once, all with the non-temporal hint; the weight row
+//   is re-read by every row and stays in L2. The sum of squares is reduced
+//   in fp32 with DPP inside the wavefront and, when WPR > 1, through WPR
+//   floats of LDS. Small rows pack RPB rows into one workgroup (the decode
+//   shapes: 1 or 32 rows).
+//
+// rmsnorm_stream - any width, any alignment (E = 1 scalar packets when the
+//   rows are not 16-byte aligned). One 256-lane workgroup per row, two passes
+//   over global memory: the first accumulates the sum of squares (and writes
+//   the rounded residual sum), the second re-reads and normalises. Used for
+//   rows wider than the register budget (> 131072 half-precision elements)
+//   and for misaligned rows.
+//
+// Numerics follow the unfused reference (ako/ops/rmsnorm_ref.py:8-50):
+//   var  = sum(x^2) * (1/H)          (fp32; 1/H rounded to fp32 on the host)
+//   rstd = rsqrt(var + eps)
+//   y    = to_T((x * rstd) * w)      (two rounded fp32 multiplies, this order)
+// and for the residual variant s = to_T(x + r) is normalised, as the
+// reference adds in the storage dtype before normalising.
+
+#include "common.h"
+#include "launch.h"
+
+namespace ako {
+
+RmsTuning g_rms_tuning;
+
+template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NT>
+__global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ rout, int64_t rows, int hidden, int64_t sx, int64_t sr,
+    int64_t sy, int64_t srout, float inv_h, float eps) {
+  constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per packet
+  constexpr int TPR = kWave * WPR;                     // lanes per row
+  using P = Pack<T, E>;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row_in_block = wave / WPR;
+  const int wave_in_row = wave - row_in_block * WPR;
+  const int t = wave_in_row * kWave + lane;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + row_in_block;
+  const bool active = row < rows;
+  const int nvec = hidden / E;
+  const int tail = hidden - nvec * E;
+
+  const T* xr = x + row * sx;
+  T* yr = y + row * sy;
+
+  P v[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int vi = t + i * TPR;
+    if (active && vi < nvec) {
+      v[i] = load_pack<T, E, NT>(xr + vi * E);
+      if constexpr (RES) {
+        const P rv = load_pack<T, E, NT>(res + row * sr + vi * E);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[i].e[e] = from_f32<T>(to_f32(v[i].e[e]) + to_f32(rv.e[e]));
+        store_pack<T, E, NT>(rout + row * srout + vi * E, v[i]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float f = to_f32(v[i].e[e]);
+        ss = __builtin_fmaf(f, f, ss);
+      }
+    }
+  }
+  // Elements past the last full packet (only when a row stride is padded).
+  T vt = from_f32<T>(0.f);
+  const int tcol = nvec * E + t;
+  const bool has_tail = active && t < tail;
+  if (has_tail) {
+    vt = xr[tcol];
+    if constexpr (RES) {
+      vt = from_f32<T>(to_f32(vt) + to_f32(res[row * sr + tcol]));
+      rout[row * srout + tcol] = vt;
+    }
+    const float f = to_f32(vt);
+    ss = __builtin_fmaf(f, f, ss);
+  }
+
+  ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    __shared__ float partial[RPB][WPR];
+    if (lane == 0) partial[row_in_block][wave_in_row] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < WPR; ++j) ss += partial[row_in_block][j];
+  }
+  const float rstd = rsqrtf(ss * inv_h + eps);
+
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int vi = t + i * TPR;
+    if (active && vi < nvec) {
+      float wf[E];
+      load_f32<W, E>(w + vi * E, wf);
+      P o;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(v[i].e[e]) * rstd) * wf[e]);
+      store_pack<T, E, NT>(yr + vi * E, o);
+    }
+  }
+  if (has_tail) yr[tcol] = from_f32<T>((to_f32(vt) * rstd) * to_f32(w[tcol]));
+}
+
+// Two-pass kernel: one workgroup of kStreamBlock lanes per row, packets of E
+// elements (E = 16/sizeof(T) when aligned, else 1).
+constexpr int kStreamBlock = 256;
+
+template <typename T, typename W, int E, bool RES>
+__global__ __launch_bounds__(kStreamBlock) void rmsnorm_stream(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ rout, int hidden, int64_t sx, int64_t sr, int64_t sy,
+    int64_t srout, float inv_h, float eps) {
+  using P = Pack<T, E>;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = hidden / E;
+  const int tail = hidden - nvec * E;
+  const T* xr = x + row * sx;
+  const T* rr = res + row * sr;  // only dereferenced when RES
+  T* yr = y + row * sy;
+  T* ror = rout + row * srout;
+
+  // s = x (+ r rounded to T); the residual variant writes s in pass one and
+  // recomputes it from the untouched inputs in pass two.
+  auto element = [&](int col) -> T {
+    if constexpr (RES) {
+      return from_f32<T>(to_f32(xr[col]) + to_f32(rr[col]));
+    } else {
+      return xr[col];
+    }
+  };
+  auto packet = [&](int vi) -> P {
+    P p = load_pack<T, E>(xr + vi * E);
+    if constexpr (RES) {
+      const P q = load_pack<T, E>(rr + vi * E);
+#pragma unroll
+      for (int e = 0; e < E; ++e) p.e[e] = from_f32<T>(to_f32(p.e[e]) + to_f32(q.e[e]));
+    }
+    return p;
+  };
+
+  float ss = 0.f;
+  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
+    const P p = packet(vi);
+    if constexpr (RES) store_pack<T, E>(ror + vi * E, p);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float f = to_f32(p.e[e]);
+      ss = __builtin_fmaf(f, f, ss);
+    }
+  }
+  for (int j = tid; j < tail; j += kStreamBlock) {
+    const T s = element(nvec * E + j);
+    if constexpr (RES) ror[nvec * E + j] = s;
+    const float f = to_f32(s);
+    ss = __builtin_fmaf(f, f, ss);
+  }
+
+  ss = wave_sum(ss);
+  __shared__ float partial[kStreamBlock / kWave];
+  if ((tid & (kWave - 1)) == 0) partial[tid / kWave] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kStreamBlock / kWave; ++j) ss += partial[j];
+  const float rstd = rsqrtf(ss * inv_h + eps);
+
+  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
+    const P p = packet(vi);
+    float wf[E];
+    load_f32<W, E>(w + vi * E, wf);
+    P o;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(p.e[e]) * rstd) * wf[e]);
+    store_pack<T, E>(yr + vi * E, o);
+  }
+  for (int j = tid; j < tail; j += kStreamBlock) {
+    const int col = nvec * E + j;
+    yr[col] = from_f32<T>((to_f32(element(col)) * rstd) * to_f32(w[col]));
+  }
+}
+
+#ifndef AKO_RMS_NT
+#define AKO_RMS_NT 1
+#endif
+
+namespace {
+
+struct RegShape {
+  int wpr, vpt;
+};
+// Instantiated (waves per row, packets per lane) shapes, smallest first.
+constexpr RegShape kRegShapes[] = {{1, 1}, {1, 2}, {1, 4}, {1, 8},  {2, 4},  {2, 8},
+                                   {4, 4}, {4, 8}, {8, 4}, {8, 8}, {16, 8}, {16, 16}};
+constexpr int kMaxRegPackets = 16 * 64 * 16;
+
+
+// Default shape: the fewest lanes that hold the row with at most 8 packets
+// per lane (16 for the widest shape).
+RegShape pick_shape(int64_t nvec) {
+  RegShape s{0, 0};
+  if (nvec <= 64) s = {1, 1};
+  else if (nvec <= 128) s = {1, 2};
+  else if (nvec <= 256) s = {1, 4};
+  else if (nvec <= 512) s = {1, 8};
+  else if (nvec <= 1024) s = {2, 8};
+  else if (nvec <= 2048) s = {4, 8};
+  else if (nvec <= 4096) s = {8, 8};
+  else if (nvec <= 8192) s = {16, 8};
+  else s = {16, 16};
+  const RmsTuning& tu = g_rms_tuning;
+  if (tu.waves_per_row > 0 || tu.vecs_per_thread > 0) {
+    RegShape want{tu.waves_per_row > 0 ? tu.waves_per_row : s.wpr,
+                  tu.vecs_per_thread > 0 ? tu.vecs_per_thread : s.vpt};
+    for (const RegShape& c : kRegShapes)
+      if (c.wpr == want.wpr && c.vpt == want.vpt && int64_t(c.wpr) * 64 * c.vpt >= nvec) return c;
+  }
+  return s;
+}
+
+template <typename T, typename W, int WPR, int VPT, bool RES>
+hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
+  constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
+  const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, RPB)));
+  const dim3 block(kWave * WPR * RPB);
+  hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0>), grid, block, 0,
+                     stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                     static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
+                     a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
+                     1.0f / static_cast<float>(a.hidden), a.eps);
+  return hipGetLastError();
+}
+
+template <typename T, typename W, bool RES>
+hipError_t run_reg_shape(const RegShape& s, const RmsArgs& a, hipStream_t stream) {
+#define AKO_RMS_SHAPE(WPR, VPT) \
+  if (s.wpr == WPR && s.vpt == VPT) return run_reg<T, W, WPR, VPT, RES>(a, stream);
+  AKO_RMS_SHAPE(1, 1)
+  AKO_RMS_SHAPE(1, 2)
+  AKO_RMS_SHAPE(1, 4)
+  AKO_RMS_SHAPE(1, 8)
+  AKO_RMS_SHAPE(2, 4)
+  AKO_RMS_SHAPE(2, 8)
+  AKO_RMS_SHAPE(4, 4)
+  AKO_RMS_SHAPE(4, 8)
+  AKO_RMS_SHAPE(8, 4)
+  AKO_RMS_SHAPE(8, 8)
+  AKO_RMS_SHAPE(16, 8)
+  AKO_RMS_SHAPE(16, 16)
+#undef AKO_RMS_SHAPE
+  return hipErrorInvalidValue;
+}
+
+template <typename T, typename W, bool RES>
+hipError_t run_stream(const RmsArgs& a, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.rows));
+  const float inv_h = 1.0f / static_cast<float>(a.hidden);
+  const auto* x = static_cast<const T*>(a.x);
+  const auto* r = static_cast<const T*>(a.r);
+  const auto* w = static_cast<const W*>(a.w);
+  auto* y = static_cast<T*>(a.y);
+  auto* ro = static_cast<T*>(a.rout);
+  const int h = static_cast<int>(a.hidden);
+  if (a.vector_ok) {
+    hipLaunchKernelGGL((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
+                       stream, x, r, w, y, ro, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
+                       w, y, ro, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, typename W>
+hipError_t run_typed(const RmsArgs& a, hipStream_t stream) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t nvec = a.hidden / E;
+  const bool reg = a.vector_ok && g_rms_tuning.force_stream == 0 && nvec <= kMaxRegPackets &&
+                   nvec >= 1;
+  if (!reg) return a.residual ? run_stream<T, W, true>(a, stream) : run_stream<T, W, false>(a, stream);
+  const RegShape s = pick_shape(nvec);
+  return a.residual ? run_reg_shape<T, W, true>(s, a, stream)
+                    : run_reg_shape<T, W, false>(s, a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const RmsArgs& a, hipStream_t stream) {
+  const bool w_same = a.w_dtype == a.dtype;
+  switch (a.dtype) {
+    case kF32:
+      return run_typed<float, float>(a, stream);
+    case kF16:
+      return w_same ? run_typed<_Float16, _Float16>(a, stream) : run_typed<_Float16, float>(a, stream);
+    case kBF16:
+      return w_same ? run_typed<__bf16, __bf16>(a, stream) : run_typed<__bf16, float>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ako

@@ -1,0 +1,230 @@
+// Rotary position embedding (neox and interleaved pairing) for gfx950.
+//
+// rope_vec - one wavefront per token (b, s). The 64 lanes of the wavefront
+//   are laid out as [heads in flight][packets per unit]:
+//     neox:        a unit is one half of a head; lane j loads packet j of the
+//                  lower half and packet j of the upper half (the pair
+//                  partners sit exactly head_dim/2 apart);
+//     interleaved: a unit is a whole head; each 16-byte packet holds E/2
+//                  complete (2i, 2i+1) pairs.
+//   A lane loads its slice of the cos/sin row once and reuses it for every
+//   head it rotates, so the tables cost one L2 read per token instead of one
+//   per head. ITERS head groups are loaded before any is computed, giving
+//   each lane up to 2*ITERS independent 16-byte loads in flight. Both tensors
+//   of a (q, k) pair can be rotated by the same wavefront (heads of the second
+//   tensor continue the head index), which is how ako_rope_qk_fwd runs in one
+//   launch.
+//
+// rope_scalar - any head_dim, any alignment: one lane per rotated pair.
+//
+// Numerics follow ako/ops/rope_ref.py:73-107: a' = a*c - b*n and
+// b' = a*n + b*c in fp32 with each product rounded separately (the library is
+// built with -ffp-contract=off), then rounded to the storage dtype.
+
+#include <algorithm>
+
+#include "common.h"
+#include "launch.h"
+
+namespace ako {
+
+RopeTuning g_rope_tuning;
+
+struct RopeTensorDev {
+  const void* x;
+  void* y;
+  int64_t heads;
+  int64_t sxb, sxs, sxh;
+  int64_t syb, sys, syh;
+};
+
+struct RopeDev {
+  RopeTensorDev t0, t1;
+  const void* cos;
+  const void* sin;
+  int64_t token0;  // first token of this launch (launches are split at 2^24 tokens)
+  int64_t tokens, seq;
+  int head_dim;
+  int64_t st;
+};
+
+template <typename T, typename TT, bool NEOX, int ITERS, int TPB>
+__global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  constexpr int NT = NEOX ? E : E / 2;  // table values per lane
+  using P = Pack<T, E>;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t token = a.token0 + static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / kWave;
+  if (token >= a.tokens) return;  // no barriers below: early exit is safe
+  const int half = a.head_dim / 2;
+  const int unit = NEOX ? half : a.head_dim;  // elements one lane group covers
+  const int per_unit = unit / E;              // packets per unit (<= 64, host-checked)
+  const int heads_per_iter = kWave / per_unit;
+  const int j = lane % per_unit;
+  const int hl = lane / per_unit;
+  if (hl >= heads_per_iter) return;
+
+  const int64_t b = token / a.seq;
+  const int64_t s = token - b * a.seq;
+  float c[NT], n[NT];
+  load_f32<TT, NT>(static_cast<const TT*>(a.cos) + s * a.st + j * NT, c);
+  load_f32<TT, NT>(static_cast<const TT*>(a.sin) + s * a.st + j * NT, n);
+
+  const int64_t total = a.t0.heads + a.t1.heads;
+  const int64_t step = static_cast<int64_t>(ITERS) * heads_per_iter;
+  for (int64_t base = 0; base < total; base += step) {
+    P lo[ITERS], hi[ITERS];
+    T* dst[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int64_t h = base + static_cast<int64_t>(it) * heads_per_iter + hl;
+      dst[it] = nullptr;
+      if (h < total) {
+        const bool first = h < a.t0.heads;
+        const RopeTensorDev& tt = first ? a.t0 : a.t1;
+        const int64_t hh = first ? h : h - a.t0.heads;
+        const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh + j * E;
+        dst[it] = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh + j * E;
+        lo[it] = load_pack<T, E, true>(src);
+        if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if (dst[it] == nullptr) continue;
+      if constexpr (NEOX) {
+        P olo, ohi;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float x0 = to_f32(lo[it].e[e]);
+          const float x1 = to_f32(hi[it].e[e]);
+          olo.e[e] = from_f32<T>(x0 * c[e] - x1 * n[e]);
+          ohi.e[e] = from_f32<T>(x0 * n[e] + x1 * c[e]);
+        }
+        store_pack<T, E, true>(dst[it], olo);
+        store_pack<T, E, true>(dst[it] + half, ohi);
+      } else {
+        P o;
+#pragma unroll
+        for (int p = 0; p < E / 2; ++p) {
+          const float x0 = to_f32(lo[it].e[2 * p]);
+          const float x1 = to_f32(lo[it].e[2 * p + 1]);
+          o.e[2 * p] = from_f32<T>(x0 * c[p] - x1 * n[p]);
+          o.e[2 * p + 1] = from_f32<T>(x0 * n[p] + x1 * c[p]);
+        }
+        store_pack<T, E, true>(dst[it], o);
+      }
+    }
+  }
+}
+
+// One lane per rotated pair; a grid-stride loop so any size fits one launch.
+template <typename T, typename TT, bool NEOX>
+__global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
+  const int half = a.head_dim / 2;
+  const int64_t total_heads = a.t0.heads + a.t1.heads;
+  const int64_t pairs = a.tokens * total_heads * half;
+  for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < pairs;
+       g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = g % half;
+    const int64_t th = g / half;
+    const int64_t h = th % total_heads;
+    const int64_t token = th / total_heads;
+    const int64_t b = token / a.seq;
+    const int64_t s = token - b * a.seq;
+    const bool first = h < a.t0.heads;
+    const RopeTensorDev& tt = first ? a.t0 : a.t1;
+    const int64_t hh = first ? h : h - a.t0.heads;
+    const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh;
+    T* dst = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh;
+    const int64_t ia = NEOX ? i : 2 * i;
+    const int64_t ib = NEOX ? i + half : 2 * i + 1;
+    const float c = to_f32(static_cast<const TT*>(a.cos)[s * a.st + i]);
+    const float n = to_f32(static_cast<const TT*>(a.sin)[s * a.st + i]);
+    const float x0 = to_f32(src[ia]);
+    const float x1 = to_f32(src[ib]);
+    dst[ia] = from_f32<T>(x0 * c - x1 * n);
+    dst[ib] = from_f32<T>(x0 * n + x1 * c);
+  }
+}
+
+namespace {
+
+RopeTensorDev to_dev(const RopeTensorArgs& t) {
+  return RopeTensorDev{t.x, t.y, t.heads, t.sxb, t.sxs, t.sxh, t.syb, t.sys, t.syh};
+}
+
+constexpr int kTokensPerBlock = 4;
+constexpr int64_t kTokensPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
+
+template <typename T, typename TT, bool NEOX, int ITERS>
+hipError_t run_vec(const RopeDev& d, hipStream_t stream) {
+  for (int64_t first = 0; first < d.tokens; first += kTokensPerLaunch) {
+    RopeDev part = d;
+    part.token0 = first;
+    const int64_t count = std::min(kTokensPerLaunch, d.tokens - first);
+    const dim3 grid(static_cast<unsigned>(ceil_div(count, kTokensPerBlock)));
+    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kTokensPerBlock>), grid,
+                       dim3(kWave * kTokensPerBlock), 0, stream, part);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+template <typename T, typename TT, bool NEOX>
+hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
+  const int64_t heads_per_iter = kWave / per_unit;
+  const int64_t total = d.t0.heads + d.t1.heads;
+  int64_t iters = ceil_div(total, heads_per_iter);
+  if (g_rope_tuning.iters > 0) iters = g_rope_tuning.iters;
+  if (iters <= 1) return run_vec<T, TT, NEOX, 1>(d, stream);
+  if (iters <= 2) return run_vec<T, TT, NEOX, 2>(d, stream);
+  if (iters <= 4) return run_vec<T, TT, NEOX, 4>(d, stream);
+  return run_vec<T, TT, NEOX, 8>(d, stream);
+}
+
+template <typename T, typename TT>
+hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
+  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, a.batch * a.seq, a.seq,
+            static_cast<int>(a.head_dim), a.st};
+  if (a.vector_ok) {
+    constexpr int E = 16 / sizeof(T);
+    const int64_t unit = a.neox ? a.head_dim / 2 : a.head_dim;
+    const int64_t per_unit = unit / E;
+    return a.neox ? run_iters<T, TT, true>(d, per_unit, stream)
+                  : run_iters<T, TT, false>(d, per_unit, stream);
+  }
+  const int64_t pairs = d.tokens * (a.t0.heads + a.t1.heads) * (a.head_dim / 2);
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(pairs, 256), 1 << 16));
+  if (a.neox) {
+    hipLaunchKernelGGL((rope_scalar<T, TT, true>), dim3(blocks), dim3(256), 0, stream, d);
+  } else {
+    hipLaunchKernelGGL((rope_scalar<T, TT, false>), dim3(blocks), dim3(256), 0, stream, d);
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t run_table(const RopeArgs& a, hipStream_t stream) {
+  switch (a.table_dtype) {
+    case kF32: return run_typed<T, float>(a, stream);
+    case kF16: return run_typed<T, _Float16>(a, stream);
+    case kBF16: return run_typed<T, __bf16>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rope(const RopeArgs& a, hipStream_t stream) {
+  switch (a.dtype) {
+    case kF32: return run_table<float>(a, stream);
+    case kF16: return run_table<_Float16>(a, stream);
+    case kBF16: return run_table<__bf16>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ako

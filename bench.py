@@ -1,0 +1,248 @@
+#!/usr/bin/env python
+"""Headline benchmark: achieved HBM bandwidth of the HIP RMSNorm kernels.
+
+One *step* is one pass of the hot path over the BASELINE.json configs[1]
+prefill grid: plain RMSNorm and residual-add RMSNorm, fp16 and bf16, hidden
+4096 / 8192 / 16384, 16384 rows (12 kernel launches, 11.27 GB of algorithmic
+traffic). Inputs are resident in HBM before timing starts; consecutive
+launches touch different buffers (11 GB per step against a 256 MB Infinity
+Cache), so every launch reads cold data. ``value`` is algorithmic bytes per
+step x steps / elapsed device time, in GB/s.
+
+Also reported on the same line:
+  roofline      the dominant kernel (largest share of the step) with its
+                per-launch duration from HIP events on the launch stream;
+  per_kernel    every launch of the step, the RoPE and SwiGLU
+                (configs[3]) prefill cells and the decode-size cells;
+  cpu_baseline  the reference's unfused PyTorch path (ako_amd.ops.*_ref) on
+                host CPU tensors, same grid, a bounded row sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+RMS_HIDDEN = (4096, 8192, 16384)
+RMS_ROWS = 16384
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true", help="skip the RoPE/SwiGLU/decode cells")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "traffic.json",
+                    help="rocprofv3 FETCH/WRITE summary for the dominant kernel (optional)")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the kernels shard "
+              "with no communication, so the N-GPU figure is N x the one-GPU figure by construction "
+              "and is not measured here.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    from ako_amd import _native
+    from ako_amd.benchmark import roofline as rf
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+    from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+    from ako_amd.ops.rope_ref import build_rope_tables
+    from ako_amd.ops.swiglu_hip import swiglu_hip
+
+    _native.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    peak = rf.hbm_peak_gbps(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape, dtype, scale=1.0, shift=0.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * scale + shift).to(dtype)
+
+    # ---- the metric's workload: configs[1] prefill grid ------------------------
+    calls = []
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        for h in RMS_HIDDEN:
+            x = rnd(RMS_ROWS, h, dtype=dtype)
+            r = rnd(RMS_ROWS, h, dtype=dtype)
+            w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
+            calls.append((f"rmsnorm_{tag}_{RMS_ROWS}x{h}", rf.alg_bytes_rmsnorm(RMS_ROWS, h, dtype),
+                          lambda x=x, w=w: rmsnorm_hip(x, w, 1e-6)))
+            calls.append((f"rmsnorm_residual_{tag}_{RMS_ROWS}x{h}",
+                          rf.alg_bytes_rmsnorm_residual(RMS_ROWS, h, dtype),
+                          lambda x=x, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
+    bytes_per_step = sum(b for _, b, _ in calls)
+    log(f"workload: {len(calls)} launches/step, {bytes_per_step / 1e9:.3f} GB/step, "
+        f"warmup {args.warmup}, steps {args.steps}")
+    rf.warm(calls, args.warmup)
+    total_ms = rf.time_steps(calls, steps=args.steps)
+    ms_per_step = total_ms / args.steps
+    value = bytes_per_step * args.steps / (total_ms * 1e-3) / 1e9
+    log(f"timed: {ms_per_step:.3f} ms/step, {value:.1f} GB/s ({100 * value / peak:.1f}% of {peak:.0f})")
+    per_launch = rf.time_each_launch(calls, steps=max(3, min(args.steps, 10)))
+    dominant = max(per_launch, key=lambda s: s.mean_ms)
+    per_kernel = [s.to_dict(peak) for s in per_launch]
+
+    roofline = {
+        "bound": "hbm",
+        "kernel": dominant.name,
+        "achieved": round(dominant.gbps(), 1),
+        "peak": peak,
+        "unit": "GB/s",
+        "frac": round(dominant.gbps() / peak, 4),
+        "traffic": None,
+        "alg_bytes_per_launch": dominant.alg_bytes,
+        "mean_launch_us": round(dominant.mean_ms * 1e3, 2),
+    }
+    if args.traffic.exists():
+        try:
+            doc = json.loads(args.traffic.read_text())
+            entry = doc.get("kernels", {}).get(dominant.name)
+            if entry:
+                roofline["traffic"] = entry["hbm_bytes_per_launch"]
+                roofline["traffic_source"] = str(args.traffic.relative_to(ROOT))
+        except (OSError, ValueError, KeyError):
+            pass
+    del calls
+    torch.cuda.empty_cache()
+
+    # ---- other configs' cells (reported, not the metric) ----------------------
+    extras = []
+    if not args.no_extras:
+        cells = []
+        for dtype in (torch.float16, torch.bfloat16):
+            tag = "fp16" if dtype == torch.float16 else "bf16"
+            for b, s in ((4, 2048), (64, 1), (1, 1)):
+                cos, sin = build_rope_tables(s, 128, device=dev)
+                cos, sin = cos.to(dtype), sin.to(dtype)
+                copies = rf.copies_for_cold(rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype), dev) if s > 1 else 1
+                qs = [rnd(b, s, 32, 128, dtype=dtype) for _ in range(copies)]
+                ks = [rnd(b, s, 8, 128, dtype=dtype) for _ in range(copies)]
+                for i in range(copies):
+                    cells.append((f"rope_q_{tag}_{b}x{s}x32x128", rf.alg_bytes_rope(b, s, 32, 128, dtype, dtype),
+                                  lambda q=qs[i], c=cos, sn=sin: rope_hip(q, c, sn, "neox")))
+                    cells.append((f"rope_k_{tag}_{b}x{s}x8x128", rf.alg_bytes_rope(b, s, 8, 128, dtype, dtype),
+                                  lambda k=ks[i], c=cos, sn=sin: rope_hip(k, c, sn, "neox")))
+                    cells.append((f"rope_qk_{tag}_{b}x{s}", rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype),
+                                  lambda q=qs[i], k=ks[i], c=cos, sn=sin: rope_qk_hip(q, k, c, sn, "neox")))
+        for m in (16384, 4096, 256, 16, 1):
+            dtype = torch.bfloat16
+            nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)
+            copies = rf.copies_for_cold(nbytes, dev) if m >= 256 else 1
+            gs = [rnd(m, 14336, dtype=dtype) for _ in range(copies)]
+            us = [rnd(m, 14336, dtype=dtype) for _ in range(copies)]
+            for i in range(copies):
+                cells.append((f"swiglu_bf16_{m}x14336", nbytes, lambda g=gs[i], u=us[i]: swiglu_hip(g, u)))
+        for dtype in (torch.float16, torch.bfloat16):
+            tag = "fp16" if dtype == torch.float16 else "bf16"
+            for rows in (1, 32):
+                for h in RMS_HIDDEN:
+                    x, r = rnd(rows, h, dtype=dtype), rnd(rows, h, dtype=dtype)
+                    w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
+                    cells.append((f"rmsnorm_{tag}_{rows}x{h}", rf.alg_bytes_rmsnorm(rows, h, dtype),
+                                  lambda x=x, w=w: rmsnorm_hip(x, w, 1e-6)))
+                    cells.append((f"rmsnorm_residual_{tag}_{rows}x{h}",
+                                  rf.alg_bytes_rmsnorm_residual(rows, h, dtype),
+                                  lambda x=x, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
+        rf.warm(cells, 2)
+        extras = [s.to_dict(peak) for s in rf.time_each_launch(cells, steps=5)]
+        log(f"extras: {len(extras)} cells timed")
+        del cells
+        torch.cuda.empty_cache()
+
+    # ---- CPU baseline: the reference's unfused PyTorch path on host cores ------
+    cpu = None
+    if not args.no_cpu:
+        from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
+
+        sample_rows = 64
+        g = torch.Generator().manual_seed(0)
+        host = []
+        for dtype in (torch.float16, torch.bfloat16):
+            for h in RMS_HIDDEN:
+                x = torch.randn(sample_rows, h, generator=g).to(dtype)
+                r = torch.randn(sample_rows, h, generator=g).to(dtype)
+                w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
+                host.append((rf.alg_bytes_rmsnorm(sample_rows, h, dtype), lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
+                host.append((rf.alg_bytes_rmsnorm_residual(sample_rows, h, dtype),
+                             lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
+        for _, fn in host:
+            fn()
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for _, fn in host:
+                fn()
+            passes += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= args.cpu_seconds and passes >= 3:
+                break
+        cpu_gbps = sum(b for b, _ in host) * passes / elapsed / 1e9
+        cpu = {
+            "value": round(cpu_gbps, 3),
+            "unit": "GB/s",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"ako_amd.ops.rmsnorm_ref / rmsnorm_residual_ref (the reference's unfused "
+                       f"PyTorch path) on CPU tensors: the same 12 cells with {sample_rows} rows "
+                       f"instead of {RMS_ROWS}, {passes} passes in {elapsed:.1f} s; "
+                       f"os.cpu_count()={os.cpu_count()}"),
+            "gpu_speedup": round(value / cpu_gbps, 1) if cpu_gbps > 0 else None,
+        }
+        log(f"cpu baseline: {cpu_gbps:.3f} GB/s on {torch.get_num_threads()} threads")
+
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) per op/shape; 4-layer decoder prefill+decode ms",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16+bf16 storage, fp32 math",
+        "data": "synthetic: x, residual ~ N(0,1), weight ~ N(1, 0.1), seeded",
+        "config": {
+            "workload": "configs[1]: RMSNorm + residual RMSNorm, fp16 and bf16, 16384 rows x "
+                        "hidden {4096, 8192, 16384}, eps 1e-6; one step = the 12 launches",
+            "rows": RMS_ROWS,
+            "hidden": list(RMS_HIDDEN),
+            "alg_bytes_per_step": bytes_per_step,
+            "pct_hbm_peak": round(100 * value / peak, 2),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_kernel": per_kernel,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

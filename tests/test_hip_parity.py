@@ -1,0 +1,299 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Every case checks two things on identical seeded inputs:
+
+* the repository's own gate against the unfused PyTorch reference run on the
+  same device (``atol + rtol(dtype) * max|ref|``, ``ako_amd.validation``), on the
+  whole output, at the BASELINE.json sizes;
+* agreement with the numpy oracle (``oracle.ops``) in ulps of ``max|ref|``:
+  at most 2 ulp for fp16/bf16 and 4 ulp for fp32 (the north-star target), on
+  the whole output where the oracle finishes in seconds and on a seeded
+  sample of rows otherwise (rows are computed independently, so sampled rows
+  of a full-size launch check that launch). Integer-like results (the rounded
+  residual sum) must match the oracle bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
+from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
+from ako_amd.ops.swiglu_hip import swiglu_hip
+from ako_amd.ops.swiglu_ref import swiglu_ref
+from ako_amd.validation.numerical import error_budget, max_abs_error_any
+from oracle import ops as oracle
+from tests._util import NAMES, to_np
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+MAX_ULPS = {torch.float16: 2.0, torch.bfloat16: 2.0, torch.float32: 4.0}
+DEV = "cuda"
+
+
+def grandn(shape, dtype, seed, *, scale=1.0, shift=0.0) -> torch.Tensor:
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device=DEV) * scale + shift).to(dtype)
+
+
+def sample_rows(n_rows: int, k: int = 256, seed: int = 0) -> np.ndarray:
+    if n_rows <= k:
+        return np.arange(n_rows)
+    rng = np.random.default_rng(seed)
+    picked = rng.choice(n_rows, size=k - 2, replace=False)
+    return np.unique(np.concatenate([[0, n_rows - 1], picked]))
+
+
+def assert_gate(ref, out) -> None:
+    err = max_abs_error_any(ref, out)
+    budget = error_budget(ref)
+    assert err <= budget, f"gate: max_error={err:.3e} > budget={budget:.3e}"
+
+
+def assert_oracle(expected: np.ndarray, got: np.ndarray, dtype: torch.dtype) -> dict:
+    report = oracle.gate(expected, got, NAMES[dtype])
+    assert report["passed"], report
+    assert report["err_ulps"] <= MAX_ULPS[dtype], report
+    return report
+
+
+# ----------------------------------------------------------------------- RMSNorm --
+
+RMS_GRID = [(rows, h) for h in (4096, 8192, 16384) for rows in (1, 32, 16384)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,hidden", RMS_GRID)
+def test_rmsnorm_config2(rows: int, hidden: int, dtype: torch.dtype) -> None:
+    x = grandn((rows, hidden), dtype, 0)
+    w = grandn((hidden,), dtype, 1, scale=0.1, shift=1.0)
+    y = rmsnorm_hip(x, w, 1e-6)
+    torch.cuda.synchronize()
+    assert y.shape == x.shape and y.dtype == dtype
+    assert_gate(rmsnorm_ref(x, w, 1e-6), y)
+    idx = sample_rows(rows)
+    sel = torch.as_tensor(idx, device=DEV)
+    expected = oracle.rmsnorm(to_np(x[sel]), to_np(w), 1e-6, dtype=NAMES[dtype])
+    assert_oracle(expected, to_np(y[sel]), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,hidden", RMS_GRID)
+def test_rmsnorm_residual_config2(rows: int, hidden: int, dtype: torch.dtype) -> None:
+    x = grandn((rows, hidden), dtype, 0)
+    r = grandn((rows, hidden), dtype, 2)
+    w = grandn((hidden,), dtype, 1, scale=0.1, shift=1.0)
+    y, s = rmsnorm_residual_hip(x, r, w, 1e-6)
+    torch.cuda.synchronize()
+    assert_gate(rmsnorm_residual_ref(x, r, w, 1e-6), (y, s))
+    idx = sample_rows(rows)
+    sel = torch.as_tensor(idx, device=DEV)
+    ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), 1e-6, dtype=NAMES[dtype])
+    np.testing.assert_array_equal(to_np(s[sel]), es)  # the rounded sum is exact
+    assert_oracle(ey, to_np(y[sel]), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 128, 1024), (2, 128, 512), (1, 2048, 4096), (3, 100),
+                                   (2, 8448), (5, 1), (4, 7), (2, 140_000), (1, 262_144)])
+def test_rmsnorm_shapes_dtypes(shape, dtype: torch.dtype) -> None:
+    """Reference test shapes, ragged widths (scalar path), rows wider than the
+    register budget (two-pass path), every dtype."""
+    x = grandn(shape, dtype, 3, scale=3.0)
+    w = grandn(shape[-1:], dtype, 4, scale=0.1, shift=1.0)
+    y = rmsnorm_hip(x, w)
+    assert_gate(rmsnorm_ref(x, w), y)
+    assert_oracle(oracle.rmsnorm(to_np(x), to_np(w), dtype=NAMES[dtype]), to_np(y), dtype)
+    r = grandn(shape, dtype, 5)
+    y2, s2 = rmsnorm_residual_hip(x, r, w)
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype=NAMES[dtype])
+    np.testing.assert_array_equal(to_np(s2), es)
+    assert_oracle(ey, to_np(y2), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rmsnorm_fp32_weight_and_strided_rows(dtype: torch.dtype) -> None:
+    base = grandn((64, 4096 + 64), dtype, 6)
+    x = base[:, :4096]  # rows 4160 elements apart, no copy
+    w = grandn((4096,), torch.float32, 7, scale=0.1, shift=1.0)
+    y = rmsnorm_hip(x, w)
+    expected = oracle.rmsnorm(to_np(x), to_np(w), dtype=NAMES[dtype], w_dtype="float32")
+    assert_oracle(expected, to_np(y), dtype)
+    # Padded stride but a width that is not a multiple of the packet: scalar tail lanes.
+    xt = base[:, :4093]
+    wt = grandn((4093,), dtype, 8, scale=0.1, shift=1.0)
+    assert_oracle(oracle.rmsnorm(to_np(xt), to_np(wt), dtype=NAMES[dtype]), to_np(rmsnorm_hip(xt, wt)), dtype)
+    # Misaligned start (offset by one element): the scalar path.
+    xm = base.reshape(-1)[1: 1 + 8 * 4096].view(8, 4096)
+    assert_oracle(oracle.rmsnorm(to_np(xm), to_np(w), dtype=NAMES[dtype], w_dtype="float32"),
+                  to_np(rmsnorm_hip(xm, w)), dtype)
+
+
+def test_rmsnorm_every_register_shape() -> None:
+    """Each instantiated (waves per row, packets per lane) shape is correct."""
+    from ako_amd import _native
+
+    x = grandn((37, 4096), torch.bfloat16, 9)
+    r = grandn((37, 4096), torch.bfloat16, 10)
+    w = grandn((4096,), torch.bfloat16, 11, scale=0.1, shift=1.0)
+    expected = oracle.rmsnorm(to_np(x), to_np(w), dtype="bfloat16")
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype="bfloat16")
+    shapes = [(1, 8), (2, 4), (2, 8), (4, 4), (4, 8), (8, 4), (8, 8), (16, 8), (16, 16)]
+    try:
+        for wpr, vpt in shapes:
+            _native.set_tuning(0, 1, wpr)
+            _native.set_tuning(0, 2, vpt)
+            assert_oracle(expected, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
+            y, s = rmsnorm_residual_hip(x, r, w)
+            np.testing.assert_array_equal(to_np(s), es)
+            assert_oracle(ey, to_np(y), torch.bfloat16)
+        _native.set_tuning(0, 1, 0)
+        _native.set_tuning(0, 2, 0)
+        _native.set_tuning(0, 3, 1)  # force the two-pass kernel
+        assert_oracle(expected, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
+    finally:
+        for key in (1, 2, 3):
+            _native.set_tuning(0, key, 0)
+
+
+def test_rmsnorm_empty_and_errors() -> None:
+    w = torch.ones(64, device=DEV, dtype=torch.float16)
+    empty = torch.empty(0, 64, device=DEV, dtype=torch.float16)
+    assert rmsnorm_hip(empty, w).shape == (0, 64)
+    with pytest.raises(ValueError, match="weight"):
+        rmsnorm_hip(torch.ones(4, 64, device=DEV, dtype=torch.float16), torch.ones(32, device=DEV))
+    with pytest.raises(ValueError, match="GPU"):
+        rmsnorm_hip(torch.ones(4, 64), torch.ones(64))
+
+
+# -------------------------------------------------------------------------- RoPE --
+
+ROPE_BS = [(1, 1), (64, 1), (4, 2048)]
+
+
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+@pytest.mark.parametrize("table_dtype", ["x", torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("batch,seq", ROPE_BS)
+def test_rope_config3(batch: int, seq: int, dtype, table_dtype, style: str) -> None:
+    tdt = dtype if table_dtype == "x" else table_dtype
+    cos, sin = build_rope_tables(seq, 128, base=10000.0, device=DEV, dtype=torch.float32)
+    cos, sin = cos.to(tdt), sin.to(tdt)
+    q = grandn((batch, seq, 32, 128), dtype, 0)
+    k = grandn((batch, seq, 8, 128), dtype, 1)
+    for t in (q, k):
+        out = rope_hip(t, cos, sin, style)
+        assert_gate(rope_ref(t, cos, sin, style), out)
+        expected = oracle.rope(to_np(t), to_np(cos), to_np(sin), style, dtype=NAMES[dtype],
+                               table_dtype=NAMES[tdt])
+        assert_oracle(expected, to_np(out), dtype)
+    qo, ko = rope_qk_hip(q, k, cos, sin, style)
+    torch.testing.assert_close(qo, rope_hip(q, cos, sin, style), rtol=0, atol=0)
+    torch.testing.assert_close(ko, rope_hip(k, cos, sin, style), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+@pytest.mark.parametrize("shape", [(2, 128, 8, 64), (1, 2048, 32, 128), (2, 6, 3, 8),
+                                   (2, 5, 3, 6), (1, 9, 4, 96), (3, 4, 2, 256)])
+def test_rope_shapes(shape, style: str, dtype) -> None:
+    """Reference test shapes plus head dims on the scalar path (6) and odd packet counts (96)."""
+    x = grandn(shape, dtype, 12)
+    cos, sin = build_rope_tables(shape[1], shape[-1], device=DEV)
+    out = rope_hip(x, cos, sin, style=style)
+    assert_gate(rope_ref(x, cos, sin, style), out)
+    assert_oracle(oracle.rope(to_np(x), to_np(cos), to_np(sin), style, dtype=NAMES[dtype]),
+                  to_np(out), dtype)
+
+
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+def test_rope_strided_views(style: str) -> None:
+    """q/k sliced out of a fused QKV projection are rotated without a copy."""
+    b, s, hq, hk, d = 2, 16, 8, 2, 128
+    qkv = grandn((b, s, (hq + 2 * hk) * d), torch.bfloat16, 13)
+    q = qkv[..., : hq * d].view(b, s, hq, d)
+    k = qkv[..., hq * d: (hq + hk) * d].view(b, s, hk, d)
+    assert not q.is_contiguous()
+    cos, sin = build_rope_tables(s, d, device=DEV)
+    full = build_rope_tables(64, d, device=DEV)
+    for t in (q, k):
+        assert_oracle(oracle.rope(to_np(t), to_np(cos), to_np(sin), style, dtype="bfloat16"),
+                      to_np(rope_hip(t, cos, sin, style)), torch.bfloat16)
+    qo, ko = rope_qk_hip(q, k, cos, sin, style)
+    assert_oracle(oracle.rope(to_np(k), to_np(cos), to_np(sin), style, dtype="bfloat16"),
+                  to_np(ko), torch.bfloat16)
+    # Tables sliced from a longer table (decode offset): row stride stays D/2.
+    c2, s2 = full[0][10:26], full[1][10:26]
+    assert_oracle(oracle.rope(to_np(q), to_np(c2), to_np(s2), style, dtype="bfloat16"),
+                  to_np(rope_hip(q, c2, s2, style)), torch.bfloat16)
+
+
+def test_rope_every_iteration_count() -> None:
+    from ako_amd import _native
+
+    x = grandn((3, 7, 40, 128), torch.float16, 14)
+    cos, sin = build_rope_tables(7, 128, device=DEV)
+    expected = oracle.rope(to_np(x), to_np(cos), to_np(sin), "neox", dtype="float16")
+    try:
+        for iters in (1, 2, 4, 8):
+            _native.set_tuning(1, 2, iters)
+            assert_oracle(expected, to_np(rope_hip(x, cos, sin)), torch.float16)
+    finally:
+        _native.set_tuning(1, 2, 0)
+
+
+def test_rope_rejects_bad_input() -> None:
+    x = torch.ones(1, 4, 2, 8, device=DEV, dtype=torch.float16)
+    cos, sin = build_rope_tables(4, 8, device=DEV)
+    with pytest.raises(ValueError):
+        rope_hip(x, cos[:2], sin[:2])
+    with pytest.raises(ValueError):
+        rope_hip(x, cos, sin, "unknown-style")
+
+
+# ------------------------------------------------------------------------ SwiGLU --
+
+
+@pytest.mark.parametrize("m", [1, 16, 256, 4096, 16384])
+def test_swiglu_config4(m: int) -> None:
+    g = grandn((m, 14336), torch.bfloat16, 0)
+    u = grandn((m, 14336), torch.bfloat16, 1)
+    y = swiglu_hip(g, u)
+    assert_gate(swiglu_ref(g, u), y)
+    sel = torch.as_tensor(sample_rows(m, 512), device=DEV)
+    assert_oracle(oracle.swiglu(to_np(g[sel]), to_np(u[sel]), dtype="bfloat16"), to_np(y[sel]),
+                  torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(8, 2048, 5632), (2, 8448), (3, 1001), (1, 1), (7,), (4, 12)])
+def test_swiglu_shapes(shape, dtype) -> None:
+    g = grandn(shape, dtype, 15, scale=4.0)
+    u = grandn(shape, dtype, 16)
+    y = swiglu_hip(g, u)
+    assert_gate(swiglu_ref(g, u), y)
+    assert_oracle(oracle.swiglu(to_np(g), to_np(u), dtype=NAMES[dtype]), to_np(y), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_swiglu_extremes_and_strides(dtype) -> None:
+    vals = torch.tensor([-100.0, -20.0, -5.0, -1.0, -0.0, 0.0, 1e-3, 1.0, 5.0, 20.0, 60.0], device=DEV)
+    g = vals.repeat(64).reshape(8, -1).to(dtype)
+    u = grandn(g.shape, dtype, 17)
+    assert_oracle(oracle.swiglu(to_np(g), to_np(u), dtype=NAMES[dtype]), to_np(swiglu_hip(g, u)), dtype)
+    base_g = grandn((16, 4096 + 8), dtype, 18)
+    base_u = grandn((16, 4096 + 8), dtype, 19)
+    gs, us = base_g[:, :4096], base_u[:, 8:]
+    assert_oracle(oracle.swiglu(to_np(gs), to_np(us), dtype=NAMES[dtype]), to_np(swiglu_hip(gs, us)), dtype)
+    gm = base_g.reshape(-1)[1:1 + 4096 * 3].view(3, 4096)  # misaligned: scalar path
+    um = base_u.reshape(-1)[3:3 + 4096 * 3].view(3, 4096)
+    assert_oracle(oracle.swiglu(to_np(gm), to_np(um), dtype=NAMES[dtype]), to_np(swiglu_hip(gm, um)), dtype)
+    empty = torch.empty(0, 14336, device=DEV, dtype=dtype)
+    assert swiglu_hip(empty, empty).shape == (0, 14336)
