@@ -42,7 +42,8 @@ struct RopeDev {
   RopeTensorDev t0, t1;
   const void* cos;
   const void* sin;
-  int64_t token0;  // first token of this launch (launches are split at 2^24 tokens)
+  int64_t wave0;   // first wavefront of this launch (launches are split at 2^24 waves)
+  int64_t chunks;  // head chunks (wavefronts) per token
   int64_t tokens, seq;
   int head_dim;
   int64_t st;
@@ -54,9 +55,12 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   constexpr int NT = NEOX ? E : E / 2;  // table values per lane
   using P = Pack<T, E>;
 
+  // Wavefront w of the grid rotates head chunk (w % chunks) of token (w / chunks).
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t token = a.token0 + static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / kWave;
+  const int64_t wave = a.wave0 + static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / kWave;
+  const int64_t token = wave / a.chunks;
   if (token >= a.tokens) return;  // no barriers below: early exit is safe
+  const int64_t chunk = wave - token * a.chunks;
   const int half = a.head_dim / 2;
   const int unit = NEOX ? half : a.head_dim;  // elements one lane group covers
   const int per_unit = unit / E;              // packets per unit (<= 64, host-checked)
@@ -72,49 +76,47 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   load_f32<TT, NT>(static_cast<const TT*>(a.sin) + s * a.st + j * NT, n);
 
   const int64_t total = a.t0.heads + a.t1.heads;
-  const int64_t step = static_cast<int64_t>(ITERS) * heads_per_iter;
-  for (int64_t base = 0; base < total; base += step) {
-    P lo[ITERS], hi[ITERS];
-    T* dst[ITERS];
+  const int64_t base = chunk * ITERS * heads_per_iter;
+  P lo[ITERS], hi[ITERS];
+  T* dst[ITERS];
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int64_t h = base + static_cast<int64_t>(it) * heads_per_iter + hl;
-      dst[it] = nullptr;
-      if (h < total) {
-        const bool first = h < a.t0.heads;
-        const RopeTensorDev& tt = first ? a.t0 : a.t1;
-        const int64_t hh = first ? h : h - a.t0.heads;
-        const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh + j * E;
-        dst[it] = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh + j * E;
-        lo[it] = load_pack<T, E, true>(src);
-        if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
-      }
+  for (int it = 0; it < ITERS; ++it) {
+    const int64_t h = base + static_cast<int64_t>(it) * heads_per_iter + hl;
+    dst[it] = nullptr;
+    if (h < total) {
+      const bool first = h < a.t0.heads;
+      const RopeTensorDev& tt = first ? a.t0 : a.t1;
+      const int64_t hh = first ? h : h - a.t0.heads;
+      const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh + j * E;
+      dst[it] = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh + j * E;
+      lo[it] = load_pack<T, E, true>(src);
+      if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
     }
+  }
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      if (dst[it] == nullptr) continue;
-      if constexpr (NEOX) {
-        P olo, ohi;
+  for (int it = 0; it < ITERS; ++it) {
+    if (dst[it] == nullptr) continue;
+    if constexpr (NEOX) {
+      P olo, ohi;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const float x0 = to_f32(lo[it].e[e]);
-          const float x1 = to_f32(hi[it].e[e]);
-          olo.e[e] = from_f32<T>(x0 * c[e] - x1 * n[e]);
-          ohi.e[e] = from_f32<T>(x0 * n[e] + x1 * c[e]);
-        }
-        store_pack<T, E, true>(dst[it], olo);
-        store_pack<T, E, true>(dst[it] + half, ohi);
-      } else {
-        P o;
-#pragma unroll
-        for (int p = 0; p < E / 2; ++p) {
-          const float x0 = to_f32(lo[it].e[2 * p]);
-          const float x1 = to_f32(lo[it].e[2 * p + 1]);
-          o.e[2 * p] = from_f32<T>(x0 * c[p] - x1 * n[p]);
-          o.e[2 * p + 1] = from_f32<T>(x0 * n[p] + x1 * c[p]);
-        }
-        store_pack<T, E, true>(dst[it], o);
+      for (int e = 0; e < E; ++e) {
+        const float x0 = to_f32(lo[it].e[e]);
+        const float x1 = to_f32(hi[it].e[e]);
+        olo.e[e] = from_f32<T>(x0 * c[e] - x1 * n[e]);
+        ohi.e[e] = from_f32<T>(x0 * n[e] + x1 * c[e]);
       }
+      store_pack<T, E, true>(dst[it], olo);
+      store_pack<T, E, true>(dst[it] + half, ohi);
+    } else {
+      P o;
+#pragma unroll
+      for (int p = 0; p < E / 2; ++p) {
+        const float x0 = to_f32(lo[it].e[2 * p]);
+        const float x1 = to_f32(lo[it].e[2 * p + 1]);
+        o.e[2 * p] = from_f32<T>(x0 * c[p] - x1 * n[p]);
+        o.e[2 * p + 1] = from_f32<T>(x0 * n[p] + x1 * c[p]);
+      }
+      store_pack<T, E, true>(dst[it], o);
     }
   }
 }
@@ -155,39 +157,43 @@ RopeTensorDev to_dev(const RopeTensorArgs& t) {
   return RopeTensorDev{t.x, t.y, t.heads, t.sxb, t.sxs, t.sxh, t.syb, t.sys, t.syh};
 }
 
-constexpr int kTokensPerBlock = 4;
-constexpr int64_t kTokensPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
+constexpr int kWavesPerBlock = 4;
+constexpr int64_t kWavesPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
 
 template <typename T, typename TT, bool NEOX, int ITERS>
-hipError_t run_vec(const RopeDev& d, hipStream_t stream) {
-  for (int64_t first = 0; first < d.tokens; first += kTokensPerLaunch) {
+hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
+  const int64_t heads_per_wave = ITERS * (kWave / per_unit);
+  d.chunks = ceil_div(d.t0.heads + d.t1.heads, heads_per_wave);
+  const int64_t waves = d.tokens * d.chunks;
+  for (int64_t first = 0; first < waves; first += kWavesPerLaunch) {
     RopeDev part = d;
-    part.token0 = first;
-    const int64_t count = std::min(kTokensPerLaunch, d.tokens - first);
-    const dim3 grid(static_cast<unsigned>(ceil_div(count, kTokensPerBlock)));
-    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kTokensPerBlock>), grid,
-                       dim3(kWave * kTokensPerBlock), 0, stream, part);
+    part.wave0 = first;
+    const int64_t count = std::min(kWavesPerLaunch, waves - first);
+    const dim3 grid(static_cast<unsigned>(ceil_div(count, kWavesPerBlock)));
+    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kWavesPerBlock>), grid,
+                       dim3(kWave * kWavesPerBlock), 0, stream, part);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   return hipSuccess;
 }
 
+// Head groups each wavefront rotates. Many short wavefronts keep the most
+// independent 16-byte requests in flight per CU (measured on MI355X: one
+// packet per lane per tensor row beats deep per-lane unrolling for pure
+// streams), so the default is one group; ako_set_tuning(1, 2, n) overrides.
 template <typename T, typename TT, bool NEOX>
 hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
-  const int64_t heads_per_iter = kWave / per_unit;
-  const int64_t total = d.t0.heads + d.t1.heads;
-  int64_t iters = ceil_div(total, heads_per_iter);
-  if (g_rope_tuning.iters > 0) iters = g_rope_tuning.iters;
-  if (iters <= 1) return run_vec<T, TT, NEOX, 1>(d, stream);
-  if (iters <= 2) return run_vec<T, TT, NEOX, 2>(d, stream);
-  if (iters <= 4) return run_vec<T, TT, NEOX, 4>(d, stream);
-  return run_vec<T, TT, NEOX, 8>(d, stream);
+  const int iters = g_rope_tuning.iters > 0 ? g_rope_tuning.iters : 1;
+  if (iters <= 1) return run_vec<T, TT, NEOX, 1>(d, per_unit, stream);
+  if (iters <= 2) return run_vec<T, TT, NEOX, 2>(d, per_unit, stream);
+  if (iters <= 4) return run_vec<T, TT, NEOX, 4>(d, per_unit, stream);
+  return run_vec<T, TT, NEOX, 8>(d, per_unit, stream);
 }
 
 template <typename T, typename TT>
 hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
-  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, a.batch * a.seq, a.seq,
+  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, 1, a.batch * a.seq, a.seq,
             static_cast<int>(a.head_dim), a.st};
   if (a.vector_ok) {
     constexpr int E = 16 / sizeof(T);

@@ -1,0 +1,170 @@
+"""The C ABI of libako_hip.so, exercised without a GPU.
+
+The library must load, export every function ``include/ako_hip.h`` declares,
+be bound to the HIP runtime PyTorch uses, and reject bad arguments with the
+documented status codes before any HIP call is made (all pointers below are
+fake addresses that the validation layer never dereferences).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from ako_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "ako_hip.h"
+OK, INVALID, UNSUPPORTED = 0, 1, 2
+F32, F16, BF16 = 0, 1, 2
+A, B, C, D, E = 0x100000, 0x200000, 0x300000, 0x400000, 0x500000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.load()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(ako_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_abi() -> None:
+    names = declared_functions()
+    assert {"ako_rmsnorm_fwd", "ako_rmsnorm_residual_fwd", "ako_rope_fwd", "ako_rope_qk_fwd",
+            "ako_swiglu_fwd", "ako_last_error", "ako_abi_version"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol(lib) -> None:
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(declared_functions()) == set(_native.SIGNATURES)
+
+
+def test_versions(lib) -> None:
+    assert lib.ako_abi_version() == _native.ABI_VERSION
+    version = lib.ako_hip_runtime_version()
+    if torch.version.hip:
+        assert version == _native._expected_runtime_version()
+    assert b"gfx950" in lib.ako_build_info()
+
+
+def rms(lib, **kw):
+    args = dict(x=A, w=B, y=C, rows=4, hidden=64, sx=64, sy=64, eps=1e-6, dt=F16, wdt=F16)
+    args.update(kw)
+    return lib.ako_rmsnorm_fwd(args["x"], args["w"], args["y"], args["rows"], args["hidden"],
+                               args["sx"], args["sy"], args["eps"], args["dt"], args["wdt"], None)
+
+
+def test_rmsnorm_validation(lib) -> None:
+    assert rms(lib, rows=0) == OK
+    assert rms(lib, hidden=0) == OK
+    assert rms(lib, dt=5) == UNSUPPORTED
+    assert rms(lib, dt=F16, wdt=BF16) == UNSUPPORTED
+    assert rms(lib, rows=-1) == INVALID
+    assert rms(lib, x=None) == INVALID
+    assert "null pointer" in _native.last_error()
+    assert rms(lib, y=A + 64) == INVALID  # y overlaps x
+    assert "overlaps" in _native.last_error()
+    assert rms(lib, sy=32) == INVALID  # output rows overlap
+    assert rms(lib, eps=-1.0) == INVALID
+    assert rms(lib, eps=float("nan")) == INVALID
+    assert rms(lib, hidden=2**31, sx=2**31, sy=2**31) == INVALID
+    assert rms(lib, sx=-64) == INVALID
+
+
+def test_rmsnorm_residual_validation(lib) -> None:
+    f = lib.ako_rmsnorm_residual_fwd
+    base = [A, B, E, C, D, 4, 64, 64, 64, 64, 64, 1e-6, BF16, F32, None]
+    assert f(*base[:5], 0, *base[6:]) == OK
+    bad = list(base)
+    bad[4] = A  # residual_out aliases x
+    assert f(*bad) == INVALID and "residual_out" in _native.last_error()
+    bad = list(base)
+    bad[1] = None
+    assert f(*bad) == INVALID
+
+
+def rope(lib, **kw):
+    a = dict(x=A, cos=B, sin=C, y=D, b=1, s=4, h=2, d=8, xs=(64, 16, 8), ys=(64, 16, 8), st=4,
+             dt=F16, tdt=F32, style=0)
+    a.update(kw)
+    return lib.ako_rope_fwd(a["x"], a["cos"], a["sin"], a["y"], a["b"], a["s"], a["h"], a["d"],
+                            *a["xs"], *a["ys"], a["st"], a["dt"], a["tdt"], a["style"], None)
+
+
+def test_rope_validation(lib) -> None:
+    assert rope(lib, b=0) == OK
+    assert rope(lib, h=0) == OK
+    assert rope(lib, d=7) == INVALID and "even" in _native.last_error()
+    assert rope(lib, style=3) == UNSUPPORTED
+    assert rope(lib, tdt=9) == UNSUPPORTED
+    assert rope(lib, cos=None) == INVALID
+    assert rope(lib, y=B) == INVALID  # output over the cos table
+    assert rope(lib, y=A) == INVALID  # output over the input
+    assert rope(lib, ys=(64, 8, 8)) == INVALID  # output tokens overlap
+    assert rope(lib, st=2) == INVALID  # table rows shorter than head_dim/2
+
+
+def test_rope_qk_validation(lib) -> None:
+    s = (ctypes.c_int64 * 3)(64, 16, 8)
+    f = lib.ako_rope_qk_fwd
+    assert f(A, B, C, D, E, E + 16, 1, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == INVALID
+    assert "two outputs overlap" in _native.last_error()
+    assert f(A, B, C, D, E, 0x600000, 0, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == OK
+    assert f(A, None, C, D, E, 0x600000, 1, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == INVALID
+
+
+def test_swiglu_validation(lib) -> None:
+    f = lib.ako_swiglu_fwd
+    assert f(A, B, C, 0, 16, 16, 16, 16, BF16, None) == OK
+    assert f(A, B, A, 4, 16, 16, 16, 16, BF16, None) == INVALID
+    assert f(A, B, C, 4, 2**31, 2**31, 2**31, 2**31, BF16, None) == INVALID
+    assert f(A, B, C, 4, 16, 16, 16, 8, BF16, None) == INVALID
+    assert f(A, B, C, 4, 16, 16, 16, 16, 7, None) == UNSUPPORTED
+    assert f(None, B, C, 4, 16, 16, 16, 16, BF16, None) == INVALID
+
+
+def test_tuning_keys(lib) -> None:
+    assert lib.ako_set_tuning(9, 1, 1) == INVALID
+    assert lib.ako_set_tuning(0, 1, -1) == INVALID
+    for op, key in ((0, 1), (0, 2), (0, 3), (1, 1), (1, 2), (2, 1), (2, 2)):
+        assert lib.ako_set_tuning(op, key, 0) == OK
+
+
+def test_status_codes_become_python_exceptions() -> None:
+    with pytest.raises(ValueError, match="ako_x"):
+        _native.check(INVALID, "ako_x")
+    with pytest.raises(RuntimeError):
+        _native.check(3, "ako_x")
+    _native.check(OK, "ako_x")
+
+
+def test_hip_candidates_refuse_cpu_tensors() -> None:
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+    from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+    from ako_amd.ops.rope_ref import build_rope_tables
+    from ako_amd.ops.swiglu_hip import swiglu_hip
+
+    x = torch.randn(2, 8, 64)
+    cos, sin = build_rope_tables(8, 16)
+    q = torch.randn(1, 8, 2, 16)
+    for call in (lambda: rmsnorm_hip(x, torch.ones(64)),
+                 lambda: rmsnorm_residual_hip(x, x, torch.ones(64)),
+                 lambda: rope_hip(q, cos, sin),
+                 lambda: rope_qk_hip(q, q, cos, sin),
+                 lambda: swiglu_hip(x, x)):
+        with pytest.raises(ValueError, match="GPU tensor"):
+            call()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path) -> None:
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setenv("AKO_HIP_LIB", str(tmp_path / "missing.so"))
+    with pytest.raises(_native.HipLibraryError, match="not built"):
+        _native.load()
+    assert not _native.is_available()

@@ -1,0 +1,133 @@
+"""Measurement utilities on the CPU: bench_op semantics, statistics, reports,
+graph capture fallbacks, regression diffs, roofline arithmetic."""
+
+from __future__ import annotations
+
+import random
+import statistics
+
+import pytest
+import torch
+
+from ako_amd.benchmark import roofline as rf
+from ako_amd.benchmark.bench_op import (
+    MAX_INNER_ITERS,
+    UNSTABLE_CV,
+    BenchResult,
+    bench_op,
+    bootstrap_ci,
+    bootstrap_ratio_ci,
+    compare_paired,
+    parse_dtypes,
+)
+from ako_amd.benchmark.env import host_cpu, sample_env
+from ako_amd.benchmark.graph import try_capture
+from ako_amd.benchmark.report import BenchmarkReport
+from ako_amd.dispatcher.hardware import get_device_info
+from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
+from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
+from ako_amd.validation.regression import compare_reports
+
+
+def test_bench_op_cpu_basics() -> None:
+    x, w = torch.randn(4, 64, 128), torch.ones(128)
+    r = bench_op(rmsnorm_ref, (x, w), warmup=2, repeats=5, kernel_name="ref")
+    assert r.latency_p50_ms > 0 and r.kernel_name == "ref" and len(r.samples_ms) == 5
+    assert r.latency_p95_ms >= r.latency_p50_ms
+    assert r.gpu_p50_ms is None and r.launch_overhead_ms is None and r.l2_state == "n/a"
+    assert "gpu_p50_ms" not in r.to_dict()
+
+
+def test_bench_op_call_kwargs_and_inner() -> None:
+    x = torch.randn(1, 8, 2, 16)
+    cos, sin = build_rope_tables(8, 16)
+    r = bench_op(rope_ref, (x, cos, sin), warmup=1, repeats=3, call_kwargs={"style": "interleaved"}, inner=3)
+    assert r.dtype == "float32" and r.inner_iters == 3
+    small = bench_op(rmsnorm_ref, (torch.randn(8, 8), torch.ones(8)), warmup=2, repeats=3)
+    assert 1 < small.inner_iters <= MAX_INNER_ITERS
+
+
+def test_bench_op_runs() -> None:
+    x, w = torch.randn(2, 16, 32), torch.ones(32)
+    single = bench_op(rmsnorm_ref, (x, w), warmup=1, repeats=4)
+    assert len(single.run_p50s) == 1 and single.to_dict()["runs"] == 1
+    many = bench_op(rmsnorm_ref, (x, w), warmup=1, repeats=4, runs=3)
+    assert len(many.run_p50s) == 3 and len(many.samples_ms) == 12 and many.iqr_ms >= 0
+
+
+def test_launch_overhead_not_clamped() -> None:
+    r = BenchResult("k", (1,), "float16", "cuda:0", 1.0, 1.0, 1.0, 0.0, [1.0], gpu_p50_ms=1.25)
+    assert r.launch_overhead_ms == pytest.approx(-0.25)
+    assert r.to_dict()["launch_overhead_ms"] == pytest.approx(-0.25)
+
+
+def test_cv_flag() -> None:
+    noisy = BenchResult("k", (1,), "f", "cpu", 1, 1, 1, 1, [1.0], run_p50s=(1.0, 2.0, 3.0, 0.5, 4.0))
+    assert noisy.cv > UNSTABLE_CV and noisy.to_dict()["unstable"] is True
+    calm = BenchResult("k", (1,), "f", "cpu", 1, 1, 1, 1, [1.0], run_p50s=(1.0, 1.02, 0.99, 1.01, 0.98))
+    assert not calm.unstable and calm.iqr_ms == pytest.approx(0.02)
+
+
+def test_bootstrap_intervals() -> None:
+    rng = random.Random(1234)
+    ratios = [1.4 * (1 + rng.uniform(-0.1, 0.1)) / (1 + rng.uniform(-0.1, 0.1)) for _ in range(30)]
+    low, high = bootstrap_ci(ratios, seed=0)
+    assert 1.0 < low < 1.4 < high
+    assert bootstrap_ci([]) == (0.0, 0.0)
+    slow = [1.4 * (1 + rng.uniform(-0.1, 0.1)) for _ in range(40)]
+    fast = [1 + rng.uniform(-0.1, 0.1) for _ in range(40)]
+    ratio, lo, hi = bootstrap_ratio_ci(slow, fast)
+    assert 1.0 < lo <= ratio <= hi
+    with pytest.raises(ValueError):
+        bootstrap_ratio_ci([], fast)
+
+
+def test_compare_paired_on_cpu() -> None:
+    x, w = torch.randn(2, 16, 32), torch.ones(32)
+    out = compare_paired(rmsnorm_ref, rmsnorm_ref, (x, w), pairs=3, warmup=1, repeats=3)
+    low, high = out["speedup_ci95"]
+    assert out["pairs"] == 3 and low <= out["speedup_median"] <= high
+
+
+def test_parse_dtypes() -> None:
+    assert parse_dtypes(["fp16", "bf16", "fp32"]) == [torch.float16, torch.bfloat16, torch.float32]
+    with pytest.raises(ValueError, match="Unknown dtype"):
+        parse_dtypes(["int8"])
+
+
+def test_report_and_regression_diff() -> None:
+    report = BenchmarkReport(operation="rmsnorm", device=get_device_info("cpu"))
+    report.add_comparison(shape=[8, 2048, 4096], baseline_ms=1.2, candidate_ms=0.3, max_error=1e-4,
+                          selected_kernel="rmsnorm_hip", dtype="float16", best_baseline_ms=0.45,
+                          best_baseline_kernel="rmsnorm_torch_native", gbps=123.0)
+    row = report.to_dict()["comparisons"][0]
+    assert row["speedup"] == 4.0 and row["speedup_vs_best_baseline"] == 1.5 and row["gbps"] == 123.0
+    slower = {"comparisons": [dict(row, candidate_ms=0.4)]}
+    assert compare_reports(slower, report.to_dict())
+    other_dtype = {"comparisons": [dict(row, candidate_ms=0.4, dtype="bfloat16")]}
+    assert compare_reports(other_dtype, report.to_dict()) == []
+
+
+def test_graph_capture_is_a_noop_on_cpu() -> None:
+    cap = try_capture(lambda t: t @ t, (torch.randn(8, 8),))
+    assert (cap.captured, cap.replay, cap.reason) == (False, None, "not_cuda")
+    r = bench_op(lambda t: t @ t, (torch.randn(16, 16),), warmup=1, repeats=2, graph=True)
+    assert r.graph_captured == 0
+
+
+def test_roofline_bytes_and_peaks() -> None:
+    assert rf.alg_bytes_rmsnorm(16384, 4096, torch.float16) == 2 * 16384 * 4096 * 2 + 4096 * 2
+    assert rf.alg_bytes_rmsnorm_residual(2, 8, torch.bfloat16, torch.float32) == 4 * 2 * 8 * 2 + 8 * 4
+    assert rf.alg_bytes_rope(4, 2048, 32, 128, torch.bfloat16, torch.float32) == 2 * 4 * 2048 * 32 * 128 * 2 + 2 * 2048 * 64 * 4
+    assert rf.alg_bytes_swiglu(16384, 14336, torch.bfloat16) == 3 * 16384 * 14336 * 2
+    assert rf.HBM_PEAK_GBPS["gfx950"] == 8000.0
+    assert rf.copies_for_cold(1) > 100 and rf.copies_for_cold(10**10) == 2
+    stats = rf.LaunchStats("k", 8_000_000_000, [1.0, 1.0])
+    assert stats.gbps() == pytest.approx(8000.0) and stats.to_dict(8000.0)["pct_hbm_peak"] == 100.0
+
+
+def test_env_samples_degrade_to_none() -> None:
+    sample = sample_env(index=99)
+    assert set(sample) == {"sm_clock_mhz", "temp_c", "power_w", "throttle_reasons"}
+    assert all(v is None for v in sample.values())
+    assert host_cpu()["os_cpu_count"] >= 1

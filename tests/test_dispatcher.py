@@ -1,0 +1,192 @@
+"""Registry and selector behaviour with plain Python candidates
+(reference tests/test_dispatcher.py:39-213)."""
+
+from __future__ import annotations
+
+import json
+import time
+from pathlib import Path
+
+import pytest
+import torch
+
+from ako_amd.dispatcher.cache import KernelCache
+from ako_amd.dispatcher.hardware import get_device_info
+from ako_amd.dispatcher.registry import KernelEntry, KernelRegistry
+from ako_amd.dispatcher.selector import BASELINE_BACKENDS, KernelSelector, shape_key
+from ako_amd.ops._registry import register_all
+from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
+
+REF = json.loads((Path(__file__).resolve().parent / "golden" / "reference_golden.json").read_text())
+
+
+def _selector(tmp_path, registry, **kw) -> KernelSelector:
+    return KernelSelector(registry=registry, cache=KernelCache(path=tmp_path / "cache.json"),
+                          warmup=1, repeats=3, **kw)
+
+
+def _registry(*entries) -> KernelRegistry:
+    reg = KernelRegistry()
+    for e in entries:
+        reg.register(e)
+    return reg
+
+
+def _baseline(fn=rmsnorm_ref, priority=10) -> KernelEntry:
+    return KernelEntry("rmsnorm", "rmsnorm_ref", fn, backend="pytorch", priority=priority)
+
+
+def test_registry_basics() -> None:
+    reg = _registry(_baseline(), _baseline())
+    assert len(reg.list_kernels("rmsnorm")) == 1
+    assert reg.list_ops() == ["rmsnorm"]
+    assert reg.get("rmsnorm", "rmsnorm_ref") is not None
+    assert reg.get("rmsnorm", "nope") is None and reg.default("nope") is None
+    reg.register(KernelEntry("rmsnorm", "low", rmsnorm_ref, backend="hip", priority=1))
+    assert reg.default("rmsnorm").kernel_name == "rmsnorm_ref"
+    assert reg.unregister("rmsnorm", "low") and not reg.unregister("rmsnorm", "low")
+
+
+def test_shape_key_format_matches_reference_records() -> None:
+    """Keys of reports/rtx3070/selected_config_{fp16,bf16}.json of the reference."""
+    for tag, dtype in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        rec = REF["selected_config_shape_keys"][tag]
+        p = rec["parameters"]
+        b, s, h = p["batch_size"], p["seq_len"], p["hidden_dim"]
+        x = torch.empty(b, s, h, dtype=dtype)
+        w = torch.empty(h, dtype=dtype)
+        assert shape_key((x, w)) == rec["shape_keys"]["rmsnorm"]
+        assert shape_key((x, x, w)) == rec["shape_keys"]["rmsnorm_residual"]
+        q = torch.empty(b, s, p["num_heads"], p["head_dim"], dtype=dtype)
+        t = torch.empty(s, p["head_dim"] // 2)
+        assert shape_key((q, t, t), p["rope_style"]) == rec["shape_keys"]["rope"]
+    x = torch.randn(2, 4)
+    assert shape_key((x,)) != shape_key((x.half(),))
+    with pytest.raises(ValueError):
+        shape_key(())
+
+
+def test_selector_default_and_unknown_op(tmp_path) -> None:
+    sel = _selector(tmp_path, _registry(_baseline()), auto_tune=False)
+    x, w = torch.randn(2, 16, 32), torch.ones(32)
+    assert sel.select("rmsnorm", x, w)(x, w).shape == x.shape
+    with pytest.raises(ValueError, match="No kernels registered"):
+        _selector(tmp_path, KernelRegistry()).select("nope", torch.randn(2))
+
+
+def test_selector_prefers_faster_valid_kernel(tmp_path) -> None:
+    def slow(x, weight, eps=1e-6):
+        time.sleep(0.002)
+        return rmsnorm_ref(x, weight, eps)
+
+    reg = _registry(_baseline(fn=slow), KernelEntry("rmsnorm", "fast", rmsnorm_ref, backend="hip", priority=5))
+    result = _selector(tmp_path, reg, allow_cpu_tuning=True).select_entry("rmsnorm", torch.randn(2, 8, 32), torch.ones(32))
+    assert result.entry.kernel_name == "fast"
+    assert result.candidates_evaluated == 2 and result.speedup > 1.0
+
+
+def test_selector_min_speedup_keeps_reference(tmp_path) -> None:
+    reg = _registry(_baseline(), KernelEntry("rmsnorm", "same", rmsnorm_ref, backend="hip", priority=5))
+    sel = _selector(tmp_path, reg, allow_cpu_tuning=True, min_speedup=1e6)
+    assert sel.select_entry("rmsnorm", torch.randn(2, 8, 32), torch.ones(32)).entry.kernel_name == "rmsnorm_ref"
+
+
+def test_selector_rejects_wrong_and_survives_broken(tmp_path) -> None:
+    def wrong(x, weight, eps=1e-6):
+        return torch.zeros_like(x)
+
+    def broken(x, weight, eps=1e-6):
+        raise RuntimeError("kernel launch failed")
+
+    reg = _registry(_baseline(), KernelEntry("rmsnorm", "wrong", wrong, backend="hip", priority=5),
+                    KernelEntry("rmsnorm", "broken", broken, backend="hip", priority=4))
+    result = _selector(tmp_path, reg, allow_cpu_tuning=True).select_entry("rmsnorm", torch.randn(2, 8, 32), torch.ones(32))
+    assert result.entry.kernel_name == "rmsnorm_ref"
+    assert any(r.startswith("wrong: max_error=") for r in result.rejected)
+    assert "broken: RuntimeError: kernel launch failed" in result.rejected
+
+
+def test_selection_is_cached_with_reference_record_keys(tmp_path) -> None:
+    reg = _registry(_baseline(), KernelEntry("rmsnorm", "alt", rmsnorm_ref, backend="hip", priority=5))
+    sel = _selector(tmp_path, reg, allow_cpu_tuning=True)
+    x, w = torch.randn(2, 8, 32), torch.ones(32)
+    first = sel.select_entry("rmsnorm", x, w)
+    second = sel.select_entry("rmsnorm", x, w)
+    assert first.source == "benchmark" and second.source == "cache" and second.from_cache
+    assert second.entry.kernel_name == first.entry.kernel_name
+    assert sel.cache.stats().hits == 1
+    record = sel.cache.get_record(get_device_info(x.device).cache_key, "rmsnorm", shape_key((x, w)))
+    assert set(record) == {"kernel", "created_at", "latency_p50_ms", "baseline_ms", "speedup",
+                           "best_baseline_ms", "best_baseline_kernel", "speedup_vs_best_baseline",
+                           "max_error", "error_budget", "backend"}
+
+
+def test_memo_hot_path(tmp_path) -> None:
+    sel = _selector(tmp_path, _registry(_baseline()), auto_tune=False)
+    w = torch.ones(32)
+    x = torch.randn(2, 8, 32)
+    for _ in range(5):
+        sel.select("rmsnorm", x, w)
+    assert sel.cache.stats().total == 1
+    sel.clear_memo()
+    sel.select("rmsnorm", x, w)
+    sel.select("rmsnorm", torch.randn(4, 8, 32), w)
+    sel.select("rmsnorm", x.half(), w)
+    sel.select("rmsnorm", x, w, extra_key="variant")
+    assert sel.cache.stats().total == 5
+
+
+def test_forced_kernel_bypasses_cache(tmp_path) -> None:
+    reg = _registry(_baseline(), KernelEntry("rmsnorm", "alt", rmsnorm_ref, backend="hip", priority=5))
+    sel = _selector(tmp_path, reg, allow_cpu_tuning=True)
+    result = sel.select_entry("rmsnorm", torch.randn(2, 8, 32), torch.ones(32), forced="alt")
+    assert (result.entry.kernel_name, result.source, len(sel.cache)) == ("alt", "forced", 0)
+    with pytest.raises(ValueError, match="Unknown kernel"):
+        sel.select_entry("rmsnorm", torch.randn(2, 8, 32), torch.ones(32), forced="nope")
+
+
+def test_selection_result_to_dict(tmp_path) -> None:
+    payload = _selector(tmp_path, _registry(_baseline()), auto_tune=False).select_entry(
+        "rmsnorm", torch.randn(2, 4), torch.ones(4)).to_dict()
+    assert (payload["selected_kernel"], payload["operation"], payload["source"]) == ("rmsnorm_ref", "rmsnorm", "default")
+    assert payload["ulp_reports"] == []
+
+
+def test_register_all_covers_every_op_with_safe_defaults() -> None:
+    reg = register_all(KernelRegistry())
+    assert reg.list_ops() == ["rmsnorm", "rmsnorm_residual", "rope", "swiglu"]
+    for op in reg.list_ops():
+        assert reg.default(op).backend == "pytorch"
+        pytorch = [k for k in reg.list_kernels(op) if k.backend == "pytorch"]
+        assert len(pytorch) == 1
+    assert "torch_native" in BASELINE_BACKENDS and "hip" not in BASELINE_BACKENDS
+    # No Triton backend anywhere.
+    assert all(k.backend != "triton" for op in reg.list_ops() for k in reg.list_kernels(op))
+
+
+def test_register_all_hip_candidates_and_opt_out(monkeypatch) -> None:
+    from ako_amd import _native
+
+    reg = register_all(KernelRegistry())
+    if _native.is_available():
+        for op in ("rmsnorm", "rmsnorm_residual", "rope", "swiglu"):
+            hip = [k for k in reg.list_kernels(op) if k.backend == "hip"]
+            assert [k.kernel_name for k in hip] == [f"{op}_hip"] and hip[0].priority == 5
+    monkeypatch.setenv("AKO_HIP_DISABLE", "1")
+    reg = register_all(KernelRegistry())
+    assert all(k.backend != "hip" for op in reg.list_ops() for k in reg.list_kernels(op))
+
+
+def test_compile_baselines_are_opt_in(monkeypatch) -> None:
+    monkeypatch.delenv("AKO_ENABLE_COMPILE", raising=False)
+    reg = register_all(KernelRegistry())
+    assert all(k.backend != "torch_compile" for op in reg.list_ops() for k in reg.list_kernels(op))
+    monkeypatch.setenv("AKO_ENABLE_COMPILE", "1")
+    reg = register_all(KernelRegistry())
+    for op in ("rmsnorm", "rmsnorm_residual", "rope", "swiglu"):
+        assert reg.get(op, f"{op}_compiled").backend == "torch_compile"
+
+
+def test_device_info_cpu() -> None:
+    info = get_device_info(torch.device("cpu"))
+    assert (info.device_type, info.compute_backend, info.cache_key) == ("cpu", "cpu", "cpu_-1")
