@@ -147,3 +147,30 @@ def warm(calls: Sequence[tuple[str, int, Callable[[], Any]]], passes: int) -> No
         for _, _, fn in calls:
             fn()
     torch.cuda.synchronize()
+
+
+def time_graph_replay(fn: Callable[[], Any], *, launches: int = 64, replays: int = 5) -> float:
+    """Device microseconds per call with host overhead removed: ``launches``
+    calls of ``fn`` are captured into one HIP graph, the graph is replayed
+    ``replays`` times between two events, and the time is divided by the
+    number of calls. Only kernels (no memsets) may be in ``fn``."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(launches):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    begin.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) * 1e3 / (launches * replays)

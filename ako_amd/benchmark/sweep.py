@@ -1,0 +1,132 @@
+"""Selection sweep over the BASELINE.json grid: which kernel wins each cell.
+
+For every cell of configs[1]-[3] (RMSNorm and residual RMSNorm, RoPE q and
+k, SwiGLU; prefill and decode sizes) a fresh ``KernelSelector`` runs the
+reference's Algorithm 1 on the GPU: the unfused reference, the PyTorch
+baselines and the HIP candidate are gated and timed (wall p50 per call,
+the reference's selection criterion), and the decision is recorded. The
+output rows follow the reference's ``comparisons[]`` format (what
+``ako/benchmark/rmsnorm_bench.py`` and ``rope_bench.py`` wrote), one report
+per operation, plus a summary with the HIP win rate.
+
+    python -m ako_amd.benchmark.sweep --out gpurun_out/selection [--ops rmsnorm,rope]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+from pathlib import Path
+from typing import Any, Iterator
+
+import torch
+
+from ako_amd.benchmark.report import BenchmarkReport, save_report
+from ako_amd.dispatcher.cache import KernelCache
+from ako_amd.dispatcher.hardware import get_device_info
+from ako_amd.dispatcher.registry import KernelRegistry
+from ako_amd.dispatcher.selector import KernelSelector
+from ako_amd.ops._registry import register_all
+from ako_amd.ops.rope_ref import build_rope_tables
+
+RMS_HIDDEN = (4096, 8192, 16384)
+RMS_ROWS = (1, 32, 16384)
+ROPE_BS = ((1, 1), (64, 1), (4, 2048))
+SWIGLU_M = (1, 16, 256, 4096, 16384)
+HALF = (torch.float16, torch.bfloat16)
+
+
+def _randn(shape, dtype, seed, device, scale=1.0, shift=0.0) -> torch.Tensor:
+    g = torch.Generator(device=device).manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device=device) * scale + shift).to(dtype)
+
+
+def cells(ops: set[str], device: torch.device) -> Iterator[tuple[str, list[int], torch.dtype, tuple, dict]]:
+    """``(op, shape, dtype, tensors, select kwargs)`` for every grid cell."""
+    for dtype in HALF:
+        for h in RMS_HIDDEN:
+            for rows in RMS_ROWS:
+                x = _randn((rows, h), dtype, 0, device)
+                w = _randn((h,), dtype, 1, device, 0.1, 1.0)
+                if "rmsnorm" in ops:
+                    yield "rmsnorm", [rows, h], dtype, (x, w), {}
+                if "rmsnorm_residual" in ops:
+                    r = _randn((rows, h), dtype, 2, device)
+                    yield "rmsnorm_residual", [rows, h], dtype, (x, r, w), {}
+    if "rope" in ops:
+        for dtype in HALF:
+            for b, s in ROPE_BS:
+                cos, sin = build_rope_tables(s, 128, device=device)
+                cos, sin = cos.to(dtype), sin.to(dtype)
+                for heads in (32, 8):
+                    x = _randn((b, s, heads, 128), dtype, 3, device)
+                    yield "rope", [b, s, heads, 128], dtype, (x, cos, sin), {
+                        "extra_key": "neox", "call_kwargs": {"style": "neox"}}
+    if "swiglu" in ops:
+        for m in SWIGLU_M:
+            g = _randn((m, 14336), torch.bfloat16, 4, device)
+            u = _randn((m, 14336), torch.bfloat16, 5, device)
+            yield "swiglu", [m, 14336], torch.bfloat16, (g, u), {}
+
+
+def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20) -> dict[str, Any]:
+    device = torch.device("cuda", torch.cuda.current_device())
+    info = get_device_info(device)
+    registry = register_all(KernelRegistry())
+    reports: dict[str, BenchmarkReport] = {}
+    wins = total = 0
+    for op, shape, dtype, tensors, kw in cells(ops, device):
+        selector = KernelSelector(registry=registry, cache=KernelCache(path=out_dir / "sweep_cache.json"),
+                                  auto_tune=True, warmup=warmup, repeats=repeats)
+        result = selector.select_entry(op, *tensors, **kw)
+        lat = dict(result.latencies_ms)
+        hip_name = f"{op}_hip"
+        hip_report = next((r for r in result.ulp_reports if r["kernel"] == hip_name), None)
+        report = reports.setdefault(op, BenchmarkReport(operation=op, device=info))
+        report.add_comparison(
+            shape=shape,
+            dtype=str(dtype).replace("torch.", ""),
+            baseline_ms=result.baseline_ms or 0.0,
+            baseline_kernel=f"{op}_ref",
+            candidate_ms=lat.get(hip_name, float("nan")),
+            max_error=hip_report["max_error"] if hip_report else None,
+            selected_kernel=result.entry.kernel_name,
+            best_baseline_ms=result.best_baseline_ms,
+            best_baseline_kernel=result.best_baseline_kernel,
+            err_ulps=hip_report["err_ulps"] if hip_report else None,
+            gate_passed=hip_report["passed"] if hip_report else None,
+            latencies_ms={k: round(v, 5) for k, v in lat.items()},
+            rejected=list(result.rejected),
+        )
+        total += 1
+        wins += int(result.entry.backend == "hip")
+        print(f"[sweep] {op:17s} {str(shape):22s} {str(dtype)[6:]:9s} -> {result.entry.kernel_name:22s} "
+              + " ".join(f"{k}={v * 1e3:.1f}us" for k, v in lat.items()), flush=True)
+        del tensors
+    out_dir.mkdir(parents=True, exist_ok=True)
+    for op, report in reports.items():
+        save_report(report, out_dir / f"selection_{op}.json")
+    summary = {"cells": total, "hip_selected": wins, "hip_win_rate": round(wins / total, 4) if total else None,
+               "gpu": info.device_name}
+    (out_dir / "selection_summary.json").write_text(json.dumps(summary, indent=2))
+    return summary
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--out", type=Path, required=True)
+    ap.add_argument("--ops", default="rmsnorm,rmsnorm_residual,rope,swiglu")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--repeats", type=int, default=20)
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("the selection sweep needs a GPU", file=sys.stderr)
+        return 1
+    summary = run(args.out, set(args.ops.split(",")), warmup=args.warmup, repeats=args.repeats)
+    print(json.dumps(summary), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -81,6 +81,8 @@ class SelectionResult:
     best_baseline_ms: float | None = None
     best_baseline_kernel: str | None = None
     ulp_reports: tuple[dict[str, Any], ...] = field(default=())
+    #: Wall p50 (ms) of every candidate that was timed, reference included.
+    latencies_ms: tuple[tuple[str, float], ...] = field(default=())
 
     @property
     def from_cache(self) -> bool:
@@ -120,6 +122,7 @@ class SelectionResult:
             "candidates_evaluated": self.candidates_evaluated,
             "rejected": list(self.rejected),
             "ulp_reports": [dict(r) for r in self.ulp_reports],
+            "latencies_ms": dict(self.latencies_ms),
         }
 
 
@@ -167,9 +170,8 @@ class KernelSelector:
             extra_key,
             x.dtype,
             x.shape,
-            x.device.type,
-            x.device.index,
-            tuple(a.shape for a in args),
+            x.device,
+            tuple([a.shape for a in args]),
         )
         fn = self._memo.get(memo_key)
         if fn is None:
@@ -263,6 +265,7 @@ class KernelSelector:
         rejected: list[str] = []
         reports: list[dict[str, Any]] = []
         baseline_ms: dict[str, float] = {reference.kernel_name: reference_ms}
+        timed: dict[str, float] = {reference.kernel_name: reference_ms}
 
         for entry in kernels:
             if entry.kernel_name == reference.kernel_name:
@@ -285,6 +288,7 @@ class KernelSelector:
                 rejected.append(f"{entry.kernel_name}: {type(exc).__name__}: {exc}")
                 continue
             evaluated += 1
+            timed[entry.kernel_name] = latency
             if entry.backend in BASELINE_BACKENDS:
                 baseline_ms[entry.kernel_name] = latency
             if latency < winner_ms and reference_ms >= latency * self.min_speedup:
@@ -322,6 +326,7 @@ class KernelSelector:
             best_baseline_ms=best_baseline_ms,
             best_baseline_kernel=best_baseline,
             ulp_reports=tuple(reports),
+            latencies_ms=tuple(timed.items()),
         )
 
 

@@ -5,48 +5,60 @@ Farx1/AKO): positional arguments, fresh outputs of the input's shape and
 dtype, inputs never written, ``ValueError`` for bad arguments and
 ``RuntimeError`` for device failures. Work goes on torch's current stream of
 the input's device, without synchronising.
+
+The per-call host path is kept short because at decode sizes (one token) the
+selector's wall-clock race against PyTorch eager is decided by host cost,
+not by the kernel: no context managers, ``empty_like`` for contiguous
+inputs, one ctypes call.
 """
 
 from __future__ import annotations
-
-import contextlib
-from typing import Iterator
 
 import torch
 
 from ako_amd import _native
 
+DT = _native.DTYPE_CODES
 _get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _get_device = getattr(torch._C, "_cuda_getDevice", None)
 
 
-def require_gpu(t: torch.Tensor, fn_name: str) -> None:
+def lib():
+    """The loaded C-ABI library (raises ``HipLibraryError`` if unusable)."""
+    return _native._lib or _native.load()
+
+
+def gpu_index(t: torch.Tensor, fn_name: str) -> int:
+    """Device index of a GPU tensor; ``ValueError`` for anything else."""
     if not t.is_cuda:
         raise ValueError(f"{fn_name} requires a GPU tensor, got device {t.device}")
+    return t.get_device()
 
 
 def dtype_code(dtype: torch.dtype, fn_name: str) -> int:
-    code = _native.DTYPE_CODES.get(dtype)
+    code = DT.get(dtype)
     if code is None:
         raise ValueError(f"{fn_name} supports float32/float16/bfloat16, got {dtype}")
     return code
 
 
-def raw_stream(device: torch.device) -> int:
+def raw_stream(index: int) -> int:
+    """Raw ``hipStream_t`` of torch's current stream on device ``index``."""
     if _get_raw_stream is not None:
-        return _get_raw_stream(device.index if device.index is not None else 0)
-    return torch.cuda.current_stream(device).cuda_stream
+        return _get_raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
-@contextlib.contextmanager
-def on_device(device: torch.device) -> Iterator[None]:
-    """Make ``device`` current for the launch when it is not already."""
-    current = _get_device() if _get_device is not None else torch.cuda.current_device()
-    if device.index is None or device.index == current:
-        yield
-    else:
-        with torch.cuda.device(device):
-            yield
+def current_device() -> int:
+    return _get_device() if _get_device is not None else torch.cuda.current_device()
+
+
+def call(index: int, fn, *args) -> int:
+    """Invoke a C-ABI entry with ``index`` as the current device."""
+    if index == current_device():
+        return fn(*args)
+    with torch.cuda.device(index):
+        return fn(*args)
 
 
 def rows_view(t: torch.Tensor) -> tuple[torch.Tensor, int]:
@@ -66,3 +78,10 @@ def rows_view(t: torch.Tensor) -> tuple[torch.Tensor, int]:
             return t, row_stride
     t = t.contiguous()
     return t, t.shape[-1]
+
+
+def empty_out(x: torch.Tensor) -> torch.Tensor:
+    """A fresh contiguous tensor of x's shape, dtype and device."""
+    if x.is_contiguous():
+        return torch.empty_like(x)
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)

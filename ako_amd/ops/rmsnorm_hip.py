@@ -14,35 +14,37 @@ from __future__ import annotations
 import torch
 
 from ako_amd import _native
-from ako_amd.ops._hip_common import dtype_code, on_device, raw_stream, require_gpu, rows_view
+from ako_amd.ops._hip_common import (
+    DT, call, dtype_code, empty_out, gpu_index, lib, raw_stream, rows_view,
+)
 
 
-def _weight(weight: torch.Tensor, x: torch.Tensor, hidden: int, fn_name: str) -> torch.Tensor:
-    if tuple(weight.shape) != (hidden,):
+def _weight(weight: torch.Tensor, index: int, dt: int, hidden: int, fn_name: str) -> tuple[torch.Tensor, int]:
+    if weight.shape != (hidden,):
         raise ValueError(f"Expected weight of shape ({hidden},), got {tuple(weight.shape)}")
-    if weight.device != x.device:
-        raise ValueError(f"{fn_name}: weight on {weight.device}, input on {x.device}")
-    if weight.dtype != x.dtype and weight.dtype != torch.float32:
-        weight = weight.float()
-    return weight if weight.is_contiguous() else weight.contiguous()
+    if not weight.is_cuda or weight.get_device() != index:
+        raise ValueError(f"{fn_name}: weight must be on the input's device")
+    wdt = DT.get(weight.dtype)
+    if wdt != dt and wdt != 0:  # neither the input dtype nor fp32
+        weight, wdt = weight.float(), 0
+    if not weight.is_contiguous():
+        weight = weight.contiguous()
+    return weight, wdt
 
 
 def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """RMSNorm over the last dimension on the GPU."""
-    require_gpu(x, "rmsnorm_hip")
+    index = gpu_index(x, "rmsnorm_hip")
     dt = dtype_code(x.dtype, "rmsnorm_hip")
     hidden = x.shape[-1] if x.dim() else 1
-    w = _weight(weight, x, hidden, "rmsnorm_hip")
+    w, wdt = _weight(weight, index, dt, hidden, "rmsnorm_hip")
     xv, sx = rows_view(x)
     rows = xv.numel() // hidden if hidden else 0
-    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    lib = _native.load()
-    with on_device(x.device):
-        status = lib.ako_rmsnorm_fwd(
-            xv.data_ptr(), w.data_ptr(), y.data_ptr(), rows, hidden, sx, hidden,
-            float(eps), dt, _native.DTYPE_CODES[w.dtype], raw_stream(x.device),
-        )
-    _native.check(status, "rmsnorm_hip")
+    y = empty_out(x)
+    status = call(index, lib().ako_rmsnorm_fwd, xv.data_ptr(), w.data_ptr(), y.data_ptr(), rows,
+                  hidden, sx, hidden, eps, dt, wdt, raw_stream(index))
+    if status:
+        _native.check(status, "rmsnorm_hip")
     return y
 
 
@@ -50,25 +52,22 @@ def rmsnorm_residual_hip(
     x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``(rmsnorm(x + residual), x + residual)`` with the sum rounded to x's dtype."""
-    require_gpu(x, "rmsnorm_residual_hip")
+    index = gpu_index(x, "rmsnorm_residual_hip")
     if x.shape != residual.shape:
         raise ValueError(f"Shape mismatch: x {tuple(x.shape)} vs residual {tuple(residual.shape)}")
-    if residual.dtype != x.dtype or residual.device != x.device:
+    if residual.dtype != x.dtype or not residual.is_cuda or residual.get_device() != index:
         raise ValueError("rmsnorm_residual_hip: residual must match x in dtype and device")
     dt = dtype_code(x.dtype, "rmsnorm_residual_hip")
     hidden = x.shape[-1] if x.dim() else 1
-    w = _weight(weight, x, hidden, "rmsnorm_residual_hip")
+    w, wdt = _weight(weight, index, dt, hidden, "rmsnorm_residual_hip")
     xv, sx = rows_view(x)
     rv, sr = rows_view(residual)
     rows = xv.numel() // hidden if hidden else 0
-    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    new_residual = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    lib = _native.load()
-    with on_device(x.device):
-        status = lib.ako_rmsnorm_residual_fwd(
-            xv.data_ptr(), rv.data_ptr(), w.data_ptr(), y.data_ptr(), new_residual.data_ptr(),
-            rows, hidden, sx, sr, hidden, hidden, float(eps), dt, _native.DTYPE_CODES[w.dtype],
-            raw_stream(x.device),
-        )
-    _native.check(status, "rmsnorm_residual_hip")
+    y = empty_out(x)
+    new_residual = empty_out(x)
+    status = call(index, lib().ako_rmsnorm_residual_fwd, xv.data_ptr(), rv.data_ptr(), w.data_ptr(),
+                  y.data_ptr(), new_residual.data_ptr(), rows, hidden, sx, sr, hidden, hidden,
+                  eps, dt, wdt, raw_stream(index))
+    if status:
+        _native.check(status, "rmsnorm_residual_hip")
     return y, new_residual

@@ -19,7 +19,7 @@ import ctypes
 import torch
 
 from ako_amd import _native
-from ako_amd.ops._hip_common import dtype_code, on_device, raw_stream, require_gpu
+from ako_amd.ops._hip_common import call, dtype_code, gpu_index, lib, raw_stream
 from ako_amd.ops.rope_ref import validate_rope_args
 
 
@@ -27,9 +27,9 @@ def _head_view(x: torch.Tensor) -> torch.Tensor:
     return x if x.stride(-1) == 1 else x.contiguous()
 
 
-def _table(t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    if t.device != x.device:
-        raise ValueError(f"rope_hip: table on {t.device}, input on {x.device}")
+def _table(t: torch.Tensor, index: int) -> torch.Tensor:
+    if not t.is_cuda or t.get_device() != index:
+        raise ValueError(f"rope_hip: tables must be on the input's device, got {t.device}")
     if t.dtype not in _native.DTYPE_CODES:
         t = t.float()
     return t if t.stride(-1) == 1 else t.contiguous()
@@ -45,24 +45,24 @@ def _table_stride(cos: torch.Tensor, sin: torch.Tensor) -> tuple[torch.Tensor, t
 def rope_hip(
     x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
 ) -> torch.Tensor:
-    require_gpu(x, "rope_hip")
+    index = gpu_index(x, "rope_hip")
     validate_rope_args(x, cos, sin, style)
     dt = dtype_code(x.dtype, "rope_hip")
     xv = _head_view(x)
-    c, s, st = _table_stride(_table(cos, x), _table(sin, x))
+    c, s, st = _table_stride(_table(cos, index), _table(sin, index))
     batch, seq, heads, head_dim = x.shape
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    lib = _native.load()
-    with on_device(x.device):
-        status = lib.ako_rope_fwd(
-            xv.data_ptr(), c.data_ptr(), s.data_ptr(), y.data_ptr(),
-            batch, seq, heads, head_dim,
-            xv.stride(0), xv.stride(1), xv.stride(2),
-            y.stride(0), y.stride(1), y.stride(2),
-            st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
-            raw_stream(x.device),
-        )
-    _native.check(status, "rope_hip")
+    status = call(
+        index, lib().ako_rope_fwd,
+        xv.data_ptr(), c.data_ptr(), s.data_ptr(), y.data_ptr(),
+        batch, seq, heads, head_dim,
+        xv.stride(0), xv.stride(1), xv.stride(2),
+        y.stride(0), y.stride(1), y.stride(2),
+        st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
+        raw_stream(index),
+    )
+    if status:
+        _native.check(status, "rope_hip")
     return y
 
 
@@ -74,27 +74,28 @@ def rope_qk_hip(
     q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Rotate ``q`` and ``k`` (same batch, seq, head_dim and dtype) in one launch."""
-    require_gpu(q, "rope_qk_hip")
+    index = gpu_index(q, "rope_qk_hip")
     validate_rope_args(q, cos, sin, style)
     validate_rope_args(k, cos, sin, style)
-    if q.shape[:2] != k.shape[:2] or q.shape[3] != k.shape[3] or q.dtype != k.dtype:
+    if (q.shape[:2] != k.shape[:2] or q.shape[3] != k.shape[3] or q.dtype != k.dtype
+            or not k.is_cuda or k.get_device() != index):
         raise ValueError(
             f"rope_qk_hip: q {tuple(q.shape)} {q.dtype} and k {tuple(k.shape)} {k.dtype} differ"
         )
     dt = dtype_code(q.dtype, "rope_qk_hip")
     qv, kv = _head_view(q), _head_view(k)
-    c, s, st = _table_stride(_table(cos, q), _table(sin, q))
+    c, s, st = _table_stride(_table(cos, index), _table(sin, index))
     batch, seq, q_heads, head_dim = q.shape
     q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
-    lib = _native.load()
-    with on_device(q.device):
-        status = lib.ako_rope_qk_fwd(
-            qv.data_ptr(), kv.data_ptr(), c.data_ptr(), s.data_ptr(),
-            q_out.data_ptr(), k_out.data_ptr(), batch, seq, q_heads, k.shape[2], head_dim,
-            _strides(qv), _strides(kv), _strides(q_out), _strides(k_out),
-            st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
-            raw_stream(q.device),
-        )
-    _native.check(status, "rope_qk_hip")
+    status = call(
+        index, lib().ako_rope_qk_fwd,
+        qv.data_ptr(), kv.data_ptr(), c.data_ptr(), s.data_ptr(),
+        q_out.data_ptr(), k_out.data_ptr(), batch, seq, q_heads, k.shape[2], head_dim,
+        _strides(qv), _strides(kv), _strides(q_out), _strides(k_out),
+        st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
+        raw_stream(index),
+    )
+    if status:
+        _native.check(status, "rope_qk_hip")
     return q_out, k_out

@@ -10,26 +10,23 @@ from __future__ import annotations
 import torch
 
 from ako_amd import _native
-from ako_amd.ops._hip_common import dtype_code, on_device, raw_stream, require_gpu, rows_view
+from ako_amd.ops._hip_common import call, dtype_code, empty_out, gpu_index, lib, raw_stream, rows_view
 
 
 def swiglu_hip(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    require_gpu(gate, "swiglu_hip")
+    index = gpu_index(gate, "swiglu_hip")
     if gate.shape != up.shape:
         raise ValueError(f"Shape mismatch: gate {tuple(gate.shape)} vs up {tuple(up.shape)}")
-    if up.dtype != gate.dtype or up.device != gate.device:
+    if up.dtype != gate.dtype or not up.is_cuda or up.get_device() != index:
         raise ValueError("swiglu_hip: up must match gate in dtype and device")
     dt = dtype_code(gate.dtype, "swiglu_hip")
     n = gate.shape[-1] if gate.dim() else 1
     gv, sg = rows_view(gate)
     uv, su = rows_view(up)
     rows = gv.numel() // n if n else 0
-    y = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
-    lib = _native.load()
-    with on_device(gate.device):
-        status = lib.ako_swiglu_fwd(
-            gv.data_ptr(), uv.data_ptr(), y.data_ptr(), rows, n, sg, su, n, dt,
-            raw_stream(gate.device),
-        )
-    _native.check(status, "swiglu_hip")
+    y = empty_out(gate)
+    status = call(index, lib().ako_swiglu_fwd, gv.data_ptr(), uv.data_ptr(), y.data_ptr(), rows, n,
+                  sg, su, n, dt, raw_stream(index))
+    if status:
+        _native.check(status, "swiglu_hip")
     return y
