@@ -174,3 +174,19 @@ def time_graph_replay(fn: Callable[[], Any], *, launches: int = 64, replays: int
     end.record()
     torch.cuda.synchronize()
     return begin.elapsed_time(end) * 1e3 / (launches * replays)
+
+
+def time_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int) -> float:
+    """Mean device milliseconds per call over ``launches`` back-to-back calls
+    cycling through ``fns`` (independent input copies), one event pair around
+    the whole loop: for kernels short enough that per-launch events would
+    distort them."""
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    begin.record(stream)
+    for i in range(launches):
+        fns[i % len(fns)]()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) / launches

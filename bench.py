@@ -44,8 +44,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-extras", action="store_true", help="skip the RoPE/SwiGLU/decode cells")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "traffic.json",
-                    help="rocprofv3 FETCH/WRITE summary for the dominant kernel (optional)")
+    ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "traffic_config2_rope_swiglu.md",
+                    help="rocprofv3 FETCH/WRITE summary (ako_amd.benchmark.rocprof) for the kernels")
     return ap.parse_args()
 
 
@@ -119,14 +119,15 @@ def main() -> int:
         "mean_launch_us": round(dominant.mean_ms * 1e3, 2),
     }
     if args.traffic.exists():
-        try:
-            doc = json.loads(args.traffic.read_text())
-            entry = doc.get("kernels", {}).get(dominant.name)
-            if entry:
-                roofline["traffic"] = entry["hbm_bytes_per_launch"]
-                roofline["traffic_source"] = str(args.traffic.relative_to(ROOT))
-        except (OSError, ValueError, KeyError):
-            pass
+        from ako_amd.benchmark.rocprof import load_traffic_md
+
+        measured = load_traffic_md(args.traffic)
+        if dominant.name in measured:
+            roofline["traffic"] = measured[dominant.name]
+            roofline["traffic_source"] = str(args.traffic.relative_to(ROOT))
+        for row in per_kernel:
+            if row["name"] in measured:
+                row["traffic_bytes"] = measured[row["name"]]
     del calls
     torch.cuda.empty_cache()
 
@@ -169,13 +170,23 @@ def main() -> int:
                                   rf.alg_bytes_rmsnorm_residual(rows, h, dtype),
                                   lambda x=x, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
         rf.warm(cells, 2)
-        extras = [s.to_dict(peak) for s in rf.time_each_launch(cells, steps=5)]
-        # Decode-size cells are launch-bound; their device time per call is
-        # measured again from a HIP graph of 64 launches (no host overhead).
-        small = {name: fn for name, nbytes, fn in cells if nbytes < 64 * 2**20}
-        for row in extras:
-            if row["name"] in small:
-                row["graph_us"] = round(rf.time_graph_replay(small[row["name"]]), 3)
+        # Each cell: 60 back-to-back launches over its input copies between one
+        # event pair (per-launch events would distort 5-30 us kernels), and for
+        # decode-size cells the device time per call from a replayed HIP graph
+        # of 64 launches (no host overhead).
+        groups: dict[str, list] = {}
+        for name, nbytes, fn in cells:
+            groups.setdefault(name, [nbytes, []])[1].append(fn)
+        for name, (nbytes, fns) in groups.items():
+            ms = rf.time_back_to_back(fns, launches=60)
+            stats = rf.LaunchStats(name, nbytes, [ms])
+            row = stats.to_dict(peak)
+            row.pop("launches")
+            row.pop("p50_us")
+            row["copies"] = len(fns)
+            if nbytes < 64 * 2**20:
+                row["graph_us"] = round(rf.time_graph_replay(fns[0]), 3)
+            extras.append(row)
         log(f"extras: {len(extras)} cells timed")
         del cells
         torch.cuda.empty_cache()
