@@ -100,6 +100,11 @@ int ako_set_tuning(int op, int key, int value) {
       if (key == 1) { ako::g_rms_tuning.waves_per_row = value; return AKO_OK; }
       if (key == 2) { ako::g_rms_tuning.vecs_per_thread = value; return AKO_OK; }
       if (key == 3) { ako::g_rms_tuning.force_stream = value; return AKO_OK; }
+      if (key == 4) {
+        if (value > 160 * 1024) return fail(AKO_ERR_INVALID_ARGUMENT, "LDS reserve above 160 KiB");
+        ako::g_rms_tuning.lds_reserve = value;
+        return AKO_OK;
+      }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

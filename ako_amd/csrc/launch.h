@@ -18,6 +18,7 @@ struct RmsTuning {
   int waves_per_row = 0;    // key 1
   int vecs_per_thread = 0;  // key 2
   int force_stream = 0;     // key 3: 1 = always use the two-pass kernel
+  int lds_reserve = 0;      // key 4: bytes of LDS reserved per workgroup (caps rows in flight per CU)
 };
 struct RopeTuning {
   int tokens_per_block = 0;  // key 1: waves (one token each) per workgroup

@@ -11,13 +11,15 @@
 //   is re-read by every row and stays in L2. The sum of squares is reduced
 //   in fp32 with DPP inside the wavefront and, when WPR > 1, through WPR
 //   floats of LDS. Small rows pack RPB rows into one workgroup (the decode
-//   shapes: 1 or 32 rows).
+//   shapes: 1 or 32 rows). A lane issues every load of a group of packets
+//   before consuming any of them, so its memory latency is paid once per
+//   group instead of once per packet.
 //
 // rmsnorm_stream - any width, any alignment (E = 1 scalar packets when the
 //   rows are not 16-byte aligned). One 256-lane workgroup per row, two passes
 //   over global memory: the first accumulates the sum of squares (and writes
 //   the rounded residual sum), the second re-reads and normalises. Used for
-//   rows wider than the register budget (> 131072 half-precision elements)
+//   rows wider than the register budget (> 65536 half-precision elements)
 //   and for misaligned rows.
 //
 // Numerics follow the unfused reference (ako/ops/rmsnorm_ref.py:8-50):
@@ -30,9 +32,26 @@
 #include "common.h"
 #include "launch.h"
 
+#ifndef AKO_RMS_PREFETCH_W
+#define AKO_RMS_PREFETCH_W 1
+#endif
+
 namespace ako {
 
 RmsTuning g_rms_tuning;
+
+// E elements of the weight row held as raw packets (one 16-byte packet, or
+// two when the weight is fp32 and the input half precision).
+template <typename W, int E>
+struct WeightPacket {
+  static constexpr int kPer = (16 / static_cast<int>(sizeof(W))) < E ? (16 / static_cast<int>(sizeof(W))) : E;
+  Pack<W, kPer> part[E / kPer];
+  __device__ __forceinline__ void load(const W* p) {
+#pragma unroll
+    for (int c = 0; c < E / kPer; ++c) part[c] = load_pack<W, kPer>(p + c * kPer);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return to_f32(part[e / kPer].e[e % kPer]); }
+};
 
 template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
@@ -41,6 +60,15 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     int64_t sy, int64_t srout, float inv_h, float eps) {
   constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per packet
   constexpr int TPR = kWave * WPR;                     // lanes per row
+  // Packets are processed in groups: every load of a group is issued before
+  // the first of them is consumed, so a lane's memory latency is paid once
+  // per group rather than once per packet. Groups stay small enough that x,
+  // the residual and the prefetched weights fit in registers.
+  constexpr int G = VPT <= 4 ? VPT : (VPT <= 8 ? 4 : 2);
+  static_assert(VPT % G == 0, "VPT must be a multiple of the group size");
+  // With few packets per lane the first weight group is fetched before the
+  // reduction; with many, registers are kept for x and weights come per group.
+  constexpr bool kPrefetchW = AKO_RMS_PREFETCH_W != 0 && VPT <= 4;
   using P = Pack<T, E>;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -59,20 +87,31 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   P v[VPT];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int vi = t + i * TPR;
-    if (active && vi < nvec) {
-      v[i] = load_pack<T, E, NTL>(xr + vi * E);
-      if constexpr (RES) {
-        const P rv = load_pack<T, E, NTL>(res + row * sr + vi * E);
+  for (int g0 = 0; g0 < VPT; g0 += G) {
+    [[maybe_unused]] P rv[G];
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[i].e[e] = from_f32<T>(to_f32(v[i].e[e]) + to_f32(rv.e[e]));
-        store_pack<T, E, NTS>(rout + row * srout + vi * E, v[i]);
+    for (int k = 0; k < G; ++k) {
+      const int vi = t + (g0 + k) * TPR;
+      if (active && vi < nvec) {
+        v[g0 + k] = load_pack<T, E, NTL>(xr + vi * E);
+        if constexpr (RES) rv[k] = load_pack<T, E, NTL>(res + row * sr + vi * E);
       }
+    }
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float f = to_f32(v[i].e[e]);
-        ss = __builtin_fmaf(f, f, ss);
+    for (int k = 0; k < G; ++k) {
+      const int vi = t + (g0 + k) * TPR;
+      if (active && vi < nvec) {
+        if constexpr (RES) {
+#pragma unroll
+          for (int e = 0; e < E; ++e)
+            v[g0 + k].e[e] = from_f32<T>(to_f32(v[g0 + k].e[e]) + to_f32(rv[k].e[e]));
+          store_pack<T, E, NTS>(rout + row * srout + vi * E, v[g0 + k]);
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float f = to_f32(v[g0 + k].e[e]);
+          ss = __builtin_fmaf(f, f, ss);
+        }
       }
     }
   }
@@ -90,6 +129,17 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     ss = __builtin_fmaf(f, f, ss);
   }
 
+  // The weight row is L2-resident (every row reads it); fetch the first group
+  // before the reduction so its latency hides behind the cross-lane sums.
+  WeightPacket<W, E> wv[G];
+  if constexpr (kPrefetchW) {
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int vi = t + k * TPR;
+      if (active && vi < nvec) wv[k].load(w + vi * E);
+    }
+  }
+
   ss = wave_sum(ss);
   if constexpr (WPR > 1) {
     __shared__ float partial[RPB][WPR];
@@ -102,15 +152,23 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   const float rstd = rsqrtf(ss * inv_h + eps);
 
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int vi = t + i * TPR;
-    if (active && vi < nvec) {
-      float wf[E];
-      load_f32<W, E>(w + vi * E, wf);
-      P o;
+  for (int g0 = 0; g0 < VPT; g0 += G) {
+    if (g0 > 0 || !kPrefetchW) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(v[i].e[e]) * rstd) * wf[e]);
-      store_pack<T, E, NTS>(yr + vi * E, o);
+      for (int k = 0; k < G; ++k) {
+        const int vi = t + (g0 + k) * TPR;
+        if (active && vi < nvec) wv[k].load(w + vi * E);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int vi = t + (g0 + k) * TPR;
+      if (active && vi < nvec) {
+        P o;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(v[g0 + k].e[e]) * rstd) * wv[k][e]);
+        store_pack<T, E, NTS>(yr + vi * E, o);
+      }
     }
   }
   if (has_tail) yr[tcol] = from_f32<T>((to_f32(vt) * rstd) * to_f32(w[tcol]));
@@ -210,25 +268,27 @@ struct RegShape {
 // Instantiated (waves per row, packets per lane) shapes, smallest first.
 constexpr RegShape kRegShapes[] = {{1, 1}, {1, 2},  {1, 4},  {1, 8},  {2, 1},  {2, 2},  {2, 4},
                                    {2, 8}, {4, 1},  {4, 2},  {4, 4},  {4, 8},  {8, 1},  {8, 2},
-                                   {8, 4}, {8, 8},  {16, 1}, {16, 2}, {16, 4}, {16, 8}, {16, 16}};
-constexpr int kMaxRegPackets = 16 * 64 * 16;
+                                   {8, 4}, {8, 8},  {16, 1}, {16, 2}, {16, 4}, {16, 8}};
+// Widest row held in registers: 16 wavefronts x 64 lanes x 8 packets (65536
+// half-precision elements). Wider rows take the two-pass kernel.
+constexpr int kMaxRegPackets = 16 * 64 * 8;
 
 
-// Default shape. Measured on MI355X (16384 rows, bf16, cold inputs): the
-// fastest shapes give each lane at most two 16-byte packets and spread a row
-// over 4-16 wavefronts; deep per-lane unrolling (8-16 packets) loses 5-15%.
+// Default shape (waves per row, packets per lane). Medians of three cold runs
+// per shape on MI355X, 16384 rows, fp16 and bf16: plain rows are fastest
+// with two packets per lane over 4-16 wavefronts; residual rows, which load
+// two tensors per packet, with one packet per lane over 8-16 wavefronts.
 // Rows that fit one wavefront's first packet stay on one wavefront so that
 // small rows need no LDS exchange and pack 4 rows per workgroup.
-RegShape pick_shape(int64_t nvec) {
-  RegShape s{16, 16};
+RegShape pick_shape(int64_t nvec, bool residual) {
+  RegShape s{16, 8};
   if (nvec <= 64) s = {1, 1};
   else if (nvec <= 128) s = {1, 2};
   else if (nvec <= 256) s = {2, 2};
-  else if (nvec <= 512) s = {4, 2};
-  else if (nvec <= 1024) s = {8, 2};
+  else if (nvec <= 512) s = residual ? RegShape{8, 1} : RegShape{4, 2};
+  else if (nvec <= 1024) s = residual ? RegShape{16, 1} : RegShape{8, 2};
   else if (nvec <= 2048) s = {16, 2};
   else if (nvec <= 4096) s = {16, 4};
-  else if (nvec <= 8192) s = {16, 8};
   const RmsTuning& tu = g_rms_tuning;
   if (tu.waves_per_row > 0 || tu.vecs_per_thread > 0) {
     RegShape want{tu.waves_per_row > 0 ? tu.waves_per_row : s.wpr,
@@ -244,7 +304,14 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
   const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, RPB)));
   const dim3 block(kWave * WPR * RPB);
-  hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid, block, 0,
+  // A residual row of >= 32 KiB per tensor keeps 4 x 32 KiB in flight; two
+  // such rows per CU exceed the CU's share of its XCD's L2 (4 MiB / 32 CUs),
+  // so an LDS reservation above half the CU's 160 KiB limits those launches to
+  // one 16-wavefront workgroup per CU (measured +2-3% at 16384 x 16384).
+  unsigned lds = static_cast<unsigned>(g_rms_tuning.lds_reserve);
+  if (lds == 0 && RES && WPR == 16 && a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024)
+    lds = 82 * 1024;
+  hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid, block, lds,
                      stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                      static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                      a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
@@ -276,7 +343,6 @@ hipError_t run_reg_shape(const RegShape& s, const RmsArgs& a, hipStream_t stream
   AKO_RMS_SHAPE(16, 2)
   AKO_RMS_SHAPE(16, 4)
   AKO_RMS_SHAPE(16, 8)
-  AKO_RMS_SHAPE(16, 16)
 #undef AKO_RMS_SHAPE
   return hipErrorInvalidValue;
 }
@@ -308,7 +374,7 @@ hipError_t run_typed(const RmsArgs& a, hipStream_t stream) {
   const bool reg = a.vector_ok && g_rms_tuning.force_stream == 0 && nvec <= kMaxRegPackets &&
                    nvec >= 1;
   if (!reg) return a.residual ? run_stream<T, W, true>(a, stream) : run_stream<T, W, false>(a, stream);
-  const RegShape s = pick_shape(nvec);
+  const RegShape s = pick_shape(nvec, a.residual);
   return a.residual ? run_reg_shape<T, W, true>(s, a, stream)
                     : run_reg_shape<T, W, false>(s, a, stream);
 }

@@ -1,0 +1,316 @@
+"""LLaMA-style decoder used to turn kernel speedups into end-to-end numbers.
+
+Mirrors ``ako/models/decoder.py:37-335`` of the reference: a stack of
+decoder layers on hidden states with two interchangeable backends,
+
+* ``"torch"`` - the unfused eager path (separate residual add, ``rmsnorm_ref``,
+  ``rope_ref``, ``F.silu(gate) * up``);
+* ``"ako"``   - the same math through the adaptive dispatcher
+  (``ako_amd.rmsnorm`` / ``rmsnorm_residual`` / ``rope`` / ``swiglu``), where
+  the gfx950 HIP kernels race the PyTorch baselines.
+
+GEMMs and attention stay on PyTorch-ROCm (hipBLASLt, SDPA) in both.
+
+Additions for BASELINE.json configs[4] (the reference stack has no embedding
+or head, ``decoder.py:261-266``): ``CausalLM`` adds a token embedding, the
+LM head and a greedy decode loop. ``KVCache`` can be preallocated to a
+maximum length (``max_len``); appending then writes into the slab instead
+of re-concatenating the whole cache on every step as ``torch.cat`` does
+(``decoder.py:84-93``); the returned views are the same.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Literal
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ako_amd.ops.rmsnorm import rmsnorm, rmsnorm_residual
+from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
+from ako_amd.ops.rope import rope
+from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
+from ako_amd.ops.swiglu import swiglu
+
+Backend = Literal["ako", "torch"]
+KernelOverride = dict[str, str]
+
+
+@dataclass
+class ModelConfig:
+    """Decoder shape (defaults: the reference's TinyLlama-like stack)."""
+
+    hidden_dim: int = 2048
+    n_layers: int = 4
+    n_heads: int = 32
+    n_kv_heads: int = 4
+    intermediate_dim: int = 5632
+    max_seq_len: int = 2048
+    rope_base: float = 10000.0
+    rope_style: str = "neox"
+    eps: float = 1e-5
+    vocab_size: int = 32000
+
+    @property
+    def head_dim(self) -> int:
+        if self.hidden_dim % self.n_heads:
+            raise ValueError(f"hidden_dim {self.hidden_dim} is not divisible by n_heads {self.n_heads}")
+        return self.hidden_dim // self.n_heads
+
+    def __post_init__(self) -> None:
+        if self.n_heads % self.n_kv_heads:
+            raise ValueError(f"n_heads {self.n_heads} is not divisible by n_kv_heads {self.n_kv_heads}")
+        if self.head_dim % 2:
+            raise ValueError(f"head_dim {self.head_dim} must be even for RoPE")
+
+
+def config5() -> ModelConfig:
+    """hidden 4096, 32 heads x 128, FFN 11008, eps 1e-6,
+    theta 1e4. Not specified there and chosen here: MHA (32 kv heads, the
+    Llama-2-7B geometry that FFN 11008 implies) and a 32000-token vocabulary."""
+    return ModelConfig(hidden_dim=4096, n_layers=4, n_heads=32, n_kv_heads=32,
+                       intermediate_dim=11008, max_seq_len=1024, rope_base=10000.0,
+                       eps=1e-6, vocab_size=32000)
+
+
+@dataclass
+class KVCache:
+    """Per-layer key/value cache, laid out ``(batch, seq, kv_heads, head_dim)``."""
+
+    n_layers: int
+    max_len: int | None = None
+    entries: list[tuple[torch.Tensor, torch.Tensor] | None] = field(default_factory=list)
+    lengths: list[int] = field(default_factory=list)
+
+    def __post_init__(self) -> None:
+        if not self.entries:
+            self.entries = [None] * self.n_layers
+        if not self.lengths:
+            self.lengths = [0] * self.n_layers
+
+    @property
+    def length(self) -> int:
+        return self.lengths[0]
+
+    def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append ``(k, v)`` and return views of the whole cache of this layer."""
+        start, add = self.lengths[layer_idx], k.shape[1]
+        if self.max_len is None:
+            prev = self.entries[layer_idx]
+            if prev is not None:
+                k = torch.cat([prev[0], k], dim=1)
+                v = torch.cat([prev[1], v], dim=1)
+            self.entries[layer_idx] = (k, v)
+            self.lengths[layer_idx] = k.shape[1]
+            return k, v
+        if start + add > self.max_len:
+            raise ValueError(f"KV cache overflow: {start + add} > max_len {self.max_len}")
+        slab = self.entries[layer_idx]
+        if slab is None:
+            shape = (k.shape[0], self.max_len, k.shape[2], k.shape[3])
+            slab = (k.new_empty(shape), v.new_empty(shape))
+            self.entries[layer_idx] = slab
+        slab[0][:, start:start + add] = k
+        slab[1][:, start:start + add] = v
+        self.lengths[layer_idx] = start + add
+        return slab[0][:, : start + add], slab[1][:, : start + add]
+
+
+def _norm(backend: Backend, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
+          eps: float, override: KernelOverride | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Residual add + RMSNorm, returning ``(normed, residual)``."""
+    override = override or {}
+    if residual is None:
+        if backend == "ako":
+            return rmsnorm(x, weight, eps, kernel=override.get("rmsnorm")), x
+        return rmsnorm_ref(x, weight, eps), x
+    if backend == "ako":
+        return rmsnorm_residual(x, residual, weight, eps, kernel=override.get("rmsnorm_residual"))
+    residual = x + residual
+    return rmsnorm_ref(residual, weight, eps), residual
+
+
+def _rope(backend: Backend, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str,
+          override: KernelOverride | None = None) -> torch.Tensor:
+    if backend != "ako":
+        return rope_ref(x, cos, sin, style)
+    return rope(x, cos, sin, style, kernel=(override or {}).get("rope"))
+
+
+class Attention(nn.Module):
+    """Grouped-query attention with RoPE and SDPA."""
+
+    def __init__(self, config: ModelConfig, backend: Backend = "ako",
+                 kernel_override: KernelOverride | None = None) -> None:
+        super().__init__()
+        self.config = config
+        self.backend = backend
+        self.kernel_override = kernel_override
+        self.repeats = config.n_heads // config.n_kv_heads
+        kv_dim = config.n_kv_heads * config.head_dim
+        self.q_proj = nn.Linear(config.hidden_dim, config.hidden_dim, bias=False)
+        self.k_proj = nn.Linear(config.hidden_dim, kv_dim, bias=False)
+        self.v_proj = nn.Linear(config.hidden_dim, kv_dim, bias=False)
+        self.o_proj = nn.Linear(config.hidden_dim, config.hidden_dim, bias=False)
+
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, layer_idx: int = 0,
+                kv_cache: KVCache | None = None) -> torch.Tensor:
+        batch, seq_len, _ = x.shape
+        cfg = self.config
+        q = self.q_proj(x).view(batch, seq_len, cfg.n_heads, cfg.head_dim)
+        k = self.k_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
+        v = self.v_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
+        q = _rope(self.backend, q, cos, sin, cfg.rope_style, self.kernel_override)
+        k = _rope(self.backend, k, cos, sin, cfg.rope_style, self.kernel_override)
+        if kv_cache is not None:
+            k, v = kv_cache.update(layer_idx, k, v)
+        if self.repeats > 1:
+            k = k.repeat_interleave(self.repeats, dim=2)
+            v = v.repeat_interleave(self.repeats, dim=2)
+        attn = F.scaled_dot_product_attention(
+            q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=seq_len > 1
+        )
+        return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
+
+
+class MLP(nn.Module):
+    """SwiGLU feed-forward network."""
+
+    def __init__(self, config: ModelConfig, backend: Backend = "ako",
+                 kernel_override: KernelOverride | None = None) -> None:
+        super().__init__()
+        self.backend = backend
+        self.kernel_override = kernel_override
+        self.gate_proj = nn.Linear(config.hidden_dim, config.intermediate_dim, bias=False)
+        self.up_proj = nn.Linear(config.hidden_dim, config.intermediate_dim, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_dim, config.hidden_dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, up = self.gate_proj(x), self.up_proj(x)
+        if self.backend == "ako":
+            act = swiglu(gate, up, kernel=(self.kernel_override or {}).get("swiglu"))
+        else:
+            act = F.silu(gate) * up
+        return self.down_proj(act)
+
+
+class DecoderLayer(nn.Module):
+    """norm -> attention -> norm -> MLP, with the residual stream carried along."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, backend: Backend = "ako",
+                 kernel_override: KernelOverride | None = None) -> None:
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.backend = backend
+        self.kernel_override = kernel_override
+        self.attention = Attention(config, backend, kernel_override)
+        self.mlp = MLP(config, backend, kernel_override)
+        self.input_norm_weight = nn.Parameter(torch.ones(config.hidden_dim))
+        self.post_attention_norm_weight = nn.Parameter(torch.ones(config.hidden_dim))
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None, cos: torch.Tensor,
+                sin: torch.Tensor, *, kv_cache: KVCache | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        eps = self.config.eps
+        x, residual = _norm(self.backend, x, residual, self.input_norm_weight, eps, self.kernel_override)
+        x = self.attention(x, cos, sin, layer_idx=self.layer_idx, kv_cache=kv_cache)
+        x, residual = _norm(self.backend, x, residual, self.post_attention_norm_weight, eps,
+                            self.kernel_override)
+        return self.mlp(x), residual
+
+
+class DecoderStack(nn.Module):
+    """Decoder layers on hidden states (no embedding, no head), final norm."""
+
+    def __init__(self, config: ModelConfig, backend: Backend = "ako",
+                 kernel_override: KernelOverride | None = None) -> None:
+        super().__init__()
+        self.config = config
+        self.backend = backend
+        self.kernel_override = kernel_override
+        self.layers = nn.ModuleList(
+            DecoderLayer(config, i, backend, kernel_override) for i in range(config.n_layers)
+        )
+        self.final_norm_weight = nn.Parameter(torch.ones(config.hidden_dim))
+        self._rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def rope_tables(self, seq_len: int, *, offset: int = 0,
+                    device: torch.device | str = "cpu") -> tuple[torch.Tensor, torch.Tensor]:
+        """fp32 ``(cos, sin)`` for positions ``[offset, offset + seq_len)``, sliced
+        from tables built once up to ``max_seq_len``."""
+        end = offset + seq_len
+        device = torch.device(device)
+        cached = self._rope_tables
+        if cached is None or cached[0].shape[0] < end or cached[0].device != device:
+            self._rope_tables = build_rope_tables(max(end, self.config.max_seq_len), self.config.head_dim,
+                                                  base=self.config.rope_base, device=device,
+                                                  dtype=torch.float32)
+        cos, sin = self._rope_tables
+        return cos[offset:end], sin[offset:end]
+
+    def forward(self, x: torch.Tensor, *, kv_cache: KVCache | None = None) -> torch.Tensor:
+        offset = kv_cache.length if kv_cache is not None else 0
+        cos, sin = self.rope_tables(x.shape[1], offset=offset, device=x.device)
+        residual: torch.Tensor | None = None
+        for layer in self.layers:
+            x, residual = layer(x, residual, cos, sin, kv_cache=kv_cache)
+        x, _ = _norm(self.backend, x, residual, self.final_norm_weight, self.config.eps,
+                     self.kernel_override)
+        return x
+
+    def new_kv_cache(self, max_len: int | None = None) -> KVCache:
+        return KVCache(n_layers=self.config.n_layers, max_len=max_len)
+
+
+def build_stack(config: ModelConfig, *, backend: Backend = "ako", device: torch.device | str = "cpu",
+                dtype: torch.dtype = torch.float32, seed: int = 0,
+                kernel_override: KernelOverride | None = None) -> DecoderStack:
+    """A stack with reproducible random weights (PyTorch's default init)."""
+    torch.manual_seed(seed)
+    model = DecoderStack(config, backend=backend, kernel_override=kernel_override)
+    return model.to(device=device, dtype=dtype).eval()
+
+
+class CausalLM(nn.Module):
+    """Token embedding -> ``DecoderStack`` -> LM head, with greedy decoding."""
+
+    def __init__(self, config: ModelConfig, backend: Backend = "ako",
+                 kernel_override: KernelOverride | None = None) -> None:
+        super().__init__()
+        self.config = config
+        self.embed = nn.Embedding(config.vocab_size, config.hidden_dim)
+        self.stack = DecoderStack(config, backend, kernel_override)
+        self.lm_head = nn.Linear(config.hidden_dim, config.vocab_size, bias=False)
+
+    def logits_last(self, ids: torch.Tensor, kv_cache: KVCache | None) -> torch.Tensor:
+        h = self.stack(self.embed(ids), kv_cache=kv_cache)
+        return self.lm_head(h[:, -1])
+
+    @torch.no_grad()
+    def generate_greedy(self, prompt: torch.Tensor, steps: int, *,
+                        kv_cache: KVCache | None = None) -> torch.Tensor:
+        """Prefill ``prompt (batch, seq)`` then ``steps`` argmax tokens; returns them."""
+        cache = kv_cache if kv_cache is not None else self.stack.new_kv_cache(prompt.shape[1] + steps)
+        nxt = self.logits_last(prompt, cache).argmax(-1, keepdim=True)
+        out = [nxt]
+        for _ in range(steps - 1):
+            nxt = self.logits_last(nxt, cache).argmax(-1, keepdim=True)
+            out.append(nxt)
+        return torch.cat(out, dim=1)
+
+
+def build_lm(config: ModelConfig, *, backend: Backend = "ako", device: torch.device | str = "cpu",
+             dtype: torch.dtype = torch.float16, seed: int = 0, init_std: float = 0.02,
+             kernel_override: KernelOverride | None = None) -> CausalLM:
+    """Random-initialised ``CausalLM``: N(0, init_std) for every Linear and the
+    embedding, ones for the norm weights (configs[4]: "random init N(0,0.02)")."""
+    torch.manual_seed(seed)
+    with torch.device(device):  # initialise in place on the target device
+        model = CausalLM(config, backend, kernel_override)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if not name.endswith("norm_weight"):
+                p.normal_(0.0, init_std)
+    return model.to(dtype=dtype).eval()

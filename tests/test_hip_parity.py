@@ -102,7 +102,7 @@ def test_rmsnorm_residual_config2(rows: int, hidden: int, dtype: torch.dtype) ->
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(2, 128, 1024), (2, 128, 512), (1, 2048, 4096), (3, 100),
-                                   (2, 8448), (5, 1), (4, 7), (2, 140_000), (1, 262_144)])
+                                   (2, 8448), (5, 1), (4, 7), (3, 65_536), (2, 65_544), (2, 140_000), (1, 262_144)])
 def test_rmsnorm_shapes_dtypes(shape, dtype: torch.dtype) -> None:
     """Reference test shapes, ragged widths (scalar path), rows wider than the
     register budget (two-pass path), every dtype."""
@@ -145,7 +145,7 @@ def test_rmsnorm_every_register_shape() -> None:
     w = grandn((4096,), torch.bfloat16, 11, scale=0.1, shift=1.0)
     expected = oracle.rmsnorm(to_np(x), to_np(w), dtype="bfloat16")
     ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype="bfloat16")
-    shapes = [(1, 8), (2, 4), (2, 8), (4, 4), (4, 8), (8, 4), (8, 8), (16, 8), (16, 16)]
+    shapes = [(1, 8), (2, 4), (2, 8), (4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4), (8, 8), (16, 1), (16, 2), (16, 4), (16, 8)]
     try:
         for wpr, vpt in shapes:
             _native.set_tuning(0, 1, wpr)

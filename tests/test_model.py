@@ -1,0 +1,72 @@
+"""The decoder harness on the CPU (reference tests/test_model.py:21-79)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from ako_amd.models.decoder import KVCache, ModelConfig, build_lm, build_stack, config5
+from ako_amd.validation.numerical import assert_close
+
+SMALL = ModelConfig(hidden_dim=64, n_layers=2, n_heads=4, n_kv_heads=2, intermediate_dim=128, max_seq_len=64)
+
+
+def test_config_validation_and_config5() -> None:
+    with pytest.raises(ValueError):
+        ModelConfig(hidden_dim=64, n_heads=6, n_kv_heads=3)
+    with pytest.raises(ValueError):
+        ModelConfig(hidden_dim=64, n_heads=4, n_kv_heads=3)
+    c = config5()
+    assert (c.hidden_dim, c.n_heads, c.head_dim, c.intermediate_dim, c.eps, c.n_layers) == (4096, 32, 128, 11008, 1e-6, 4)
+
+
+def test_backends_agree_and_shapes() -> None:
+    x = torch.randn(2, 8, SMALL.hidden_dim)
+    ako_out = build_stack(SMALL, backend="ako", seed=7)(x)
+    torch_out = build_stack(SMALL, backend="torch", seed=7)(x)
+    assert ako_out.shape == (2, 8, SMALL.hidden_dim) and torch.isfinite(ako_out).all()
+    assert_close(ako_out, torch_out, atol=1e-5, rtol=1e-5)
+
+
+def test_attention_is_causal() -> None:
+    model = build_stack(SMALL, backend="ako", seed=3)
+    x = torch.randn(1, 8, SMALL.hidden_dim)
+    changed = x.clone()
+    changed[:, 5:] += 1.0
+    base, other = model(x), model(changed)
+    assert_close(base[:, :5], other[:, :5], atol=1e-5, rtol=1e-5)
+    assert not torch.allclose(base[:, 5:], other[:, 5:])
+
+
+@pytest.mark.parametrize("max_len", [None, 16])
+def test_kv_cache_decode_matches_prefill(max_len) -> None:
+    model = build_stack(SMALL, backend="ako", seed=11)
+    x = torch.randn(1, 6, SMALL.hidden_dim)
+    prefill = model(x)
+    cache = model.new_kv_cache(max_len)
+    decoded = torch.cat([model(x[:, i:i + 1], kv_cache=cache) for i in range(6)], dim=1)
+    assert cache.length == 6
+    assert_close(decoded, prefill, atol=1e-4, rtol=1e-4)
+
+
+def test_kv_cache_growth_and_overflow() -> None:
+    cache = KVCache(n_layers=2)
+    k = torch.randn(1, 1, 2, 8)
+    cache.update(0, k, k)
+    cache.update(0, k, k)
+    assert cache.length == 2 and cache.entries[1] is None
+    fixed = KVCache(n_layers=1, max_len=2)
+    fixed.update(0, k, k)
+    kk, _ = fixed.update(0, k, k)
+    assert kk.shape[1] == 2
+    with pytest.raises(ValueError, match="overflow"):
+        fixed.update(0, k, k)
+
+
+def test_greedy_generation_backends_agree() -> None:
+    cfg = ModelConfig(hidden_dim=64, n_layers=2, n_heads=4, n_kv_heads=4, intermediate_dim=96,
+                      max_seq_len=32, vocab_size=50, eps=1e-6)
+    prompt = torch.randint(0, 50, (1, 7), generator=torch.Generator().manual_seed(0))
+    a = build_lm(cfg, backend="ako", dtype=torch.float32, seed=5).generate_greedy(prompt, 6)
+    b = build_lm(cfg, backend="torch", dtype=torch.float32, seed=5).generate_greedy(prompt, 6)
+    assert a.shape == (1, 6) and torch.equal(a, b)
