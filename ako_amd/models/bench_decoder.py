@@ -6,7 +6,9 @@ RMSNorm / residual RMSNorm / RoPE / SwiGLU go through the ``ako_amd``
 dispatcher (``backend="ako"``) or the unfused eager references
 (``backend="torch"``). Reported per backend: prefill ms, decode ms (all 128
 steps and per step), wall clock around a synchronised region, plus the
-generated tokens so the two backends can be compared.
+generated tokens so the two backends can be compared. Each backend is also
+run with every decode step replayed from a HIP graph (``GraphedGreedy``),
+which removes the per-launch host cost that dominates batch-1 decoding.
 
     python -m ako_amd.models.bench_decoder [--steps 128] [--prompt 512]
 """
@@ -21,7 +23,7 @@ from typing import Any
 
 import torch
 
-from ako_amd.models.decoder import build_lm, config5
+from ako_amd.models.decoder import GraphedGreedy, build_lm, config5
 
 
 def _timed(fn) -> tuple[Any, float]:
@@ -33,7 +35,7 @@ def _timed(fn) -> tuple[Any, float]:
 
 
 def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3,
-                device: str = "cuda", seed: int = 0) -> dict[str, Any]:
+                device: str = "cuda", seed: int = 0, graphed: bool = True) -> dict[str, Any]:
     cfg = config5()
     cfg.max_seq_len = prompt_len + decode_steps
     model = build_lm(cfg, backend=backend, device=device, dtype=torch.float16, seed=seed)
@@ -57,8 +59,23 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
             tokens, t_dec = _timed(decode)
             prefill_ms.append(t_pre)
             decode_ms.append(t_dec)
+        graphed_ms, graphed_tokens = [], None
+        if graphed:
+            for _ in range(repeats):
+                runner = GraphedGreedy(model, prompt, decode_steps)
+                graphed_tokens, t_g = _timed(runner.run)
+                graphed_ms.append(t_g)
+                del runner
     prefill = sorted(prefill_ms)[len(prefill_ms) // 2]
     dec = sorted(decode_ms)[len(decode_ms) // 2]
+    extra = {}
+    if graphed_ms:
+        g = sorted(graphed_ms)[len(graphed_ms) // 2]
+        extra = {
+            "graphed_decode_ms": round(g, 3),
+            "graphed_decode_ms_per_step": round(g / max(decode_steps - 1, 1), 4),
+            "graphed_tokens_match_eager": bool(torch.equal(graphed_tokens.cpu(), tokens.cpu())),
+        }
     return {
         "backend": backend,
         "prefill_ms": round(prefill, 3),
@@ -67,6 +84,7 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
         "prompt_len": prompt_len,
         "decode_steps": decode_steps,
         "tokens": tokens[0].tolist(),
+        **extra,
     }
 
 
@@ -83,6 +101,9 @@ def compare(prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3) ->
         "ako": results["ako"],
         "prefill_speedup": round(results["torch"]["prefill_ms"] / results["ako"]["prefill_ms"], 3),
         "decode_speedup": round(results["torch"]["decode_ms"] / results["ako"]["decode_ms"], 3),
+        "graphed_decode_speedup": (
+            round(results["torch"]["graphed_decode_ms"] / results["ako"]["graphed_decode_ms"], 3)
+            if "graphed_decode_ms" in results["ako"] else None),
         "greedy_tokens_identical": first_diff is None,
         "first_token_mismatch": first_diff,
     }

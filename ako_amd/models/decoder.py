@@ -118,6 +118,63 @@ class KVCache:
         return slab[0][:, : start + add], slab[1][:, : start + add]
 
 
+class StaticKVCache:
+    """Fixed-shape key/value cache for HIP-graph-captured decoding.
+
+    Slabs are laid out heads-major, ``(batch, kv_heads, max_len, head_dim)``,
+    so attention reads them without a transposed view. The current length
+    lives on the device (``pos``), so a decode step has static shapes and can
+    be captured once and replayed: keys and values are written at ``pos``
+    with ``index_copy_``, attention covers all ``max_len`` slots under an
+    additive mask (0 for filled slots, -inf beyond ``pos``), and the RoPE row
+    for ``pos`` is gathered from the full table on the device. Multi-token
+    calls (prefill) take the host-tracked path with causal attention.
+    """
+
+    def __init__(self, n_layers: int, batch: int, kv_heads: int, head_dim: int, max_len: int,
+                 *, dtype: torch.dtype, device: torch.device | str) -> None:
+        self.n_layers = n_layers
+        self.max_len = max_len
+        shape = (batch, kv_heads, max_len, head_dim)
+        self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
+        self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
+        self.pos = torch.zeros(1, dtype=torch.long, device=device)
+        self.host_len = 0
+        self.slots = torch.arange(max_len, device=device)
+        self.mask = torch.zeros(1, 1, 1, max_len, dtype=dtype, device=device)
+
+    @property
+    def length(self) -> int:
+        return self.host_len
+
+    def begin_step(self) -> None:
+        """Refresh the attention mask from ``pos`` (device-side, capturable)."""
+        filled = self.slots <= self.pos
+        self.mask.copy_(torch.where(filled, 0.0, float("-inf")).to(self.mask.dtype).view(1, 1, 1, -1))
+
+    def end_step(self, tokens: int) -> None:
+        self.pos.add_(tokens)
+
+    def rope_rows(self, cos_full: torch.Tensor, sin_full: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        return cos_full.index_select(0, self.pos), sin_full.index_select(0, self.pos)
+
+    def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor):
+        """Store ``(k, v)`` given as ``(batch, seq, heads, dim)``; returns heads-major
+        ``(keys, values, mask, causal)`` for attention."""
+        n = k.shape[1]
+        if n == 1:
+            self.k[layer_idx].index_copy_(2, self.pos, k.transpose(1, 2))
+            self.v[layer_idx].index_copy_(2, self.pos, v.transpose(1, 2))
+            return self.k[layer_idx], self.v[layer_idx], self.mask, False
+        start = self.host_len
+        if start + n > self.max_len:
+            raise ValueError(f"KV cache overflow: {start + n} > max_len {self.max_len}")
+        self.k[layer_idx][:, :, start:start + n] = k.transpose(1, 2)
+        self.v[layer_idx][:, :, start:start + n] = v.transpose(1, 2)
+        end = start + n
+        return self.k[layer_idx][:, :, :end], self.v[layer_idx][:, :, :end], None, start == 0
+
+
 def _norm(backend: Backend, x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
           eps: float, override: KernelOverride | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Residual add + RMSNorm, returning ``(normed, residual)``."""
@@ -164,6 +221,14 @@ class Attention(nn.Module):
         v = self.v_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
         q = _rope(self.backend, q, cos, sin, cfg.rope_style, self.kernel_override)
         k = _rope(self.backend, k, cos, sin, cfg.rope_style, self.kernel_override)
+        if isinstance(kv_cache, StaticKVCache):
+            kh, vh, mask, causal = kv_cache.update(layer_idx, k, v)
+            if self.repeats > 1:
+                kh = kh.repeat_interleave(self.repeats, dim=1)
+                vh = vh.repeat_interleave(self.repeats, dim=1)
+            attn = F.scaled_dot_product_attention(q.transpose(1, 2), kh, vh, attn_mask=mask,
+                                                  is_causal=causal and mask is None)
+            return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
         if kv_cache is not None:
             k, v = kv_cache.update(layer_idx, k, v)
         if self.repeats > 1:
@@ -250,15 +315,32 @@ class DecoderStack(nn.Module):
         cos, sin = self._rope_tables
         return cos[offset:end], sin[offset:end]
 
-    def forward(self, x: torch.Tensor, *, kv_cache: KVCache | None = None) -> torch.Tensor:
-        offset = kv_cache.length if kv_cache is not None else 0
-        cos, sin = self.rope_tables(x.shape[1], offset=offset, device=x.device)
+    def forward(self, x: torch.Tensor, *, kv_cache: KVCache | StaticKVCache | None = None) -> torch.Tensor:
+        static_step = isinstance(kv_cache, StaticKVCache) and x.shape[1] == 1
+        if static_step:
+            full = self.rope_tables(self.config.max_seq_len, device=x.device)
+            cos, sin = kv_cache.rope_rows(*full)
+            kv_cache.begin_step()
+        else:
+            offset = kv_cache.length if kv_cache is not None else 0
+            cos, sin = self.rope_tables(x.shape[1], offset=offset, device=x.device)
         residual: torch.Tensor | None = None
         for layer in self.layers:
             x, residual = layer(x, residual, cos, sin, kv_cache=kv_cache)
         x, _ = _norm(self.backend, x, residual, self.final_norm_weight, self.config.eps,
                      self.kernel_override)
+        if isinstance(kv_cache, StaticKVCache):
+            if static_step:
+                kv_cache.end_step(1)
+            else:
+                kv_cache.host_len += x.shape[1]
+                kv_cache.pos.fill_(kv_cache.host_len)
         return x
+
+    def new_static_cache(self, max_len: int, *, batch: int = 1) -> StaticKVCache:
+        p = next(self.parameters())
+        return StaticKVCache(self.config.n_layers, batch, self.config.n_kv_heads, self.config.head_dim,
+                             max_len, dtype=p.dtype, device=p.device)
 
     def new_kv_cache(self, max_len: int | None = None) -> KVCache:
         return KVCache(n_layers=self.config.n_layers, max_len=max_len)
@@ -299,6 +381,59 @@ class CausalLM(nn.Module):
             nxt = self.logits_last(nxt, cache).argmax(-1, keepdim=True)
             out.append(nxt)
         return torch.cat(out, dim=1)
+
+
+class GraphedGreedy:
+    """Greedy decoding with every decode step replayed from one HIP graph.
+
+    The prompt is prefilled eagerly into a ``StaticKVCache``; one eager decode
+    step then runs on a side stream (kernel selection and allocator warmup
+    happen there, and its cache slot is rewritten by the first real step),
+    and the next step is captured. Each replay reads the token in ``ids``,
+    writes the next one back into ``ids`` and into ``history``, and advances
+    the device-side position, so decoding needs no host work per token
+    beyond the replay call.
+    """
+
+    def __init__(self, model: "CausalLM", prompt: torch.Tensor, steps: int) -> None:
+        if prompt.shape[0] != 1:
+            raise ValueError("graphed decoding is written for batch 1")
+        self.model = model
+        self.steps = steps
+        self.prompt_len = prompt.shape[1]
+        max_len = self.prompt_len + steps
+        if model.config.max_seq_len < max_len:
+            raise ValueError(f"max_seq_len {model.config.max_seq_len} < prompt + steps {max_len}")
+        self.cache = model.stack.new_static_cache(max_len)
+        self.ids = model.logits_last(prompt, self.cache).argmax(-1, keepdim=True)
+        self.history = torch.zeros(steps, dtype=torch.long, device=prompt.device)
+        self.history[:1] = self.ids.view(1)
+        self.base = torch.full((1,), self.prompt_len - 1, dtype=torch.long, device=prompt.device)
+
+        first = self.ids.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._step()
+            self.cache.pos.sub_(1)  # undo the warmup step: position and token
+            self.ids.copy_(first)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+
+    def _step(self) -> None:
+        nxt = self.model.logits_last(self.ids, self.cache).argmax(-1, keepdim=True)
+        self.ids.copy_(nxt)
+        # pos has advanced past the token just produced: its index is pos - prompt_len.
+        self.history.index_copy_(0, self.cache.pos - self.base - 1, nxt.view(1))
+
+    @torch.no_grad()
+    def run(self) -> torch.Tensor:
+        for _ in range(self.steps - 1):
+            self.graph.replay()
+        return self.history.view(1, -1)
 
 
 def build_lm(config: ModelConfig, *, backend: Backend = "ako", device: torch.device | str = "cpu",

@@ -14,6 +14,9 @@ Also reported on the same line:
                 per-launch duration from HIP events on the launch stream;
   per_kernel    every launch of the step, the RoPE and SwiGLU
                 (configs[3]) prefill cells and the decode-size cells;
+  decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
+                128 greedy steps, eager PyTorch vs the dispatcher, each also
+                with decode steps replayed from a HIP graph;
   cpu_baseline  the reference's unfused PyTorch path (ako_amd.ops.*_ref) on
                 host CPU tensors, same grid, a bounded row sample.
 
@@ -43,6 +46,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="skip the RoPE/SwiGLU/decode cells")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the configs[4] decoder run")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "traffic_config2_rope_swiglu.md",
                     help="rocprofv3 FETCH/WRITE summary (ako_amd.benchmark.rocprof) for the kernels")
@@ -191,6 +195,17 @@ def main() -> int:
         del cells
         torch.cuda.empty_cache()
 
+    # ---- the 4-layer decoder, prefill 512 + 128 greedy steps -------
+    decoder = None
+    if not args.no_decoder:
+        from ako_amd.models.bench_decoder import compare
+
+        decoder = compare(prompt_len=512, decode_steps=128, repeats=3)
+        log(f"decoder: prefill {decoder['torch']['prefill_ms']} -> {decoder['ako']['prefill_ms']} ms, "
+            f"decode/step {decoder['torch']['decode_ms_per_step']} -> {decoder['ako']['decode_ms_per_step']} ms "
+            f"(graphed {decoder['ako'].get('graphed_decode_ms_per_step')} ms)")
+        torch.cuda.empty_cache()
+
     # ---- CPU baseline: the reference's unfused PyTorch path on host cores ------
     cpu = None
     if not args.no_cpu:
@@ -254,6 +269,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "decoder": decoder,
         "per_kernel": per_kernel,
         "extras": extras,
     }

@@ -70,3 +70,25 @@ def test_greedy_generation_backends_agree() -> None:
     a = build_lm(cfg, backend="ako", dtype=torch.float32, seed=5).generate_greedy(prompt, 6)
     b = build_lm(cfg, backend="torch", dtype=torch.float32, seed=5).generate_greedy(prompt, 6)
     assert a.shape == (1, 6) and torch.equal(a, b)
+
+
+def test_static_cache_decode_matches_cat_cache() -> None:
+    cfg = ModelConfig(hidden_dim=64, n_layers=2, n_heads=4, n_kv_heads=2, intermediate_dim=96,
+                      max_seq_len=32, vocab_size=50, eps=1e-6)
+    model = build_lm(cfg, backend="ako", dtype=torch.float32, seed=5)
+    prompt = torch.randint(0, 50, (1, 7), generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        cat_cache = model.stack.new_kv_cache()
+        static = model.stack.new_static_cache(16)
+        h_cat = model.logits_last(prompt, cat_cache)
+        h_static = model.logits_last(prompt, static)
+        assert_close(h_static, h_cat, atol=1e-5, rtol=1e-5)
+        ids = h_cat.argmax(-1, keepdim=True)
+        for _ in range(5):
+            a = model.logits_last(ids, cat_cache)
+            b = model.logits_last(ids, static)
+            assert_close(b, a, atol=1e-5, rtol=1e-5)
+            ids = a.argmax(-1, keepdim=True)
+    assert int(static.pos) == 12 and static.length == 7
+    with pytest.raises(ValueError, match="overflow"):
+        static.update(0, torch.zeros(1, 20, 2, 16), torch.zeros(1, 20, 2, 16))
