@@ -35,7 +35,6 @@ ROPE_STYLE_CODES = {"neox": 0, "interleaved": 1}
 
 #: Every symbol the header declares, with its (restype, argtypes).
 _i64, _int, _ptr, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
-_i64p = ctypes.POINTER(ctypes.c_int64)
 SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "ako_abi_version": (_int, []),
     "ako_hip_runtime_version": (_int, []),
@@ -51,10 +50,12 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _int, _int, _int, _ptr],
     ),
+    # The four stride arguments are `const int64_t*`; they are passed as
+    # addresses into one ctypes array (c_void_p) to keep the call cheap.
     "ako_rope_qk_fwd": (
         _int,
-        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p,
-         _i64p, _i64, _int, _int, _int, _ptr],
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
+         _ptr, _i64, _int, _int, _int, _ptr],
     ),
     "ako_swiglu_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _int, _ptr]),
     "ako_set_tuning": (_int, [_int, _int, _int]),

@@ -54,14 +54,19 @@ def cells(ops: set[str], device: torch.device) -> Iterator[tuple[str, list[int],
                 if "rmsnorm_residual" in ops:
                     r = _randn((rows, h), dtype, 2, device)
                     yield "rmsnorm_residual", [rows, h], dtype, (x, r, w), {}
-    if "rope" in ops:
+    if "rope" in ops or "rope_qk" in ops:
         for dtype in HALF:
             for b, s in ROPE_BS:
                 cos, sin = build_rope_tables(s, 128, device=device)
                 cos, sin = cos.to(dtype), sin.to(dtype)
-                for heads in (32, 8):
-                    x = _randn((b, s, heads, 128), dtype, 3, device)
-                    yield "rope", [b, s, heads, 128], dtype, (x, cos, sin), {
+                q = _randn((b, s, 32, 128), dtype, 3, device)
+                k = _randn((b, s, 8, 128), dtype, 6, device)
+                if "rope" in ops:
+                    for x in (q, k):
+                        yield "rope", list(x.shape), dtype, (x, cos, sin), {
+                            "extra_key": "neox", "call_kwargs": {"style": "neox"}}
+                if "rope_qk" in ops:
+                    yield "rope_qk", [b, s, 32 + 8, 128], dtype, (q, k, cos, sin), {
                         "extra_key": "neox", "call_kwargs": {"style": "neox"}}
     if "swiglu" in ops:
         for m in SWIGLU_M:
@@ -116,7 +121,7 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20) -> 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--out", type=Path, required=True)
-    ap.add_argument("--ops", default="rmsnorm,rmsnorm_residual,rope,swiglu")
+    ap.add_argument("--ops", default="rmsnorm,rmsnorm_residual,rope,rope_qk,swiglu")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--repeats", type=int, default=20)
     args = ap.parse_args(argv)

@@ -212,6 +212,8 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
   }
   if (batch == 0 || seq == 0 || head_dim == 0 || total_heads == 0) return AKO_OK;
   if (head_dim > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: head_dim too large", fn);
+  if (batch > kMaxInt / seq || total_heads > kMaxInt)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: batch*seq and the head count must stay below 2^31", fn);
   if (!cos || !sin) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null table pointer", fn);
   if (st < head_dim / 2 && seq > 1) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: table row stride %lld < head_dim/2", fn, (long long)st);
   const int eb = ako::dtype_bytes(dtype);

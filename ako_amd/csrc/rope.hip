@@ -42,11 +42,14 @@ struct RopeDev {
   RopeTensorDev t0, t1;
   const void* cos;
   const void* sin;
-  int64_t wave0;   // first wavefront of this launch (launches are split at 2^24 waves)
-  int64_t chunks;  // head chunks (wavefronts) per token
-  int64_t tokens, seq;
+  int token0;        // first token of this launch (launches split at token boundaries)
+  int tokens;        // tokens in this launch
+  int chunks;        // head chunks (wavefronts) per token
+  int seq;
   int head_dim;
+  int pu_shift;      // log2(packets per unit) when a power of two, else -1
   int64_t st;
+  int64_t total_tokens;  // batch * seq (scalar kernel)
 };
 
 template <typename T, typename TT, bool NEOX, int ITERS, int TPB>
@@ -55,33 +58,43 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   constexpr int NT = NEOX ? E : E / 2;  // table values per lane
   using P = Pack<T, E>;
 
-  // Wavefront w of the grid rotates head chunk (w % chunks) of token (w / chunks).
+  // Wavefront w of this launch rotates head chunk (w % chunks) of token
+  // token0 + w / chunks. All index arithmetic is 32-bit (the host splits
+  // launches so that w < 2^24 and validates batch * seq < 2^31).
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave = a.wave0 + static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / kWave;
-  const int64_t token = wave / a.chunks;
-  if (token >= a.tokens) return;  // no barriers below: early exit is safe
-  const int64_t chunk = wave - token * a.chunks;
+  const int wave = static_cast<int>(blockIdx.x) * TPB + static_cast<int>(threadIdx.x) / kWave;
+  const int tl = wave / a.chunks;
+  if (tl >= a.tokens) return;  // no barriers below: early exit is safe
+  const int chunk = wave - tl * a.chunks;
+  const int token = a.token0 + tl;
   const int half = a.head_dim / 2;
   const int unit = NEOX ? half : a.head_dim;  // elements one lane group covers
   const int per_unit = unit / E;              // packets per unit (<= 64, host-checked)
-  const int heads_per_iter = kWave / per_unit;
-  const int j = lane % per_unit;
-  const int hl = lane / per_unit;
+  int j, hl, heads_per_iter;
+  if (a.pu_shift >= 0) {
+    j = lane & (per_unit - 1);
+    hl = lane >> a.pu_shift;
+    heads_per_iter = kWave >> a.pu_shift;
+  } else {
+    j = lane % per_unit;
+    hl = lane / per_unit;
+    heads_per_iter = kWave / per_unit;
+  }
   if (hl >= heads_per_iter) return;
 
-  const int64_t b = token / a.seq;
-  const int64_t s = token - b * a.seq;
+  const int b = token / a.seq;
+  const int s = token - b * a.seq;
   float c[NT], n[NT];
   load_f32<TT, NT>(static_cast<const TT*>(a.cos) + s * a.st + j * NT, c);
   load_f32<TT, NT>(static_cast<const TT*>(a.sin) + s * a.st + j * NT, n);
 
-  const int64_t total = a.t0.heads + a.t1.heads;
-  const int64_t base = chunk * ITERS * heads_per_iter;
+  const int total = static_cast<int>(a.t0.heads + a.t1.heads);
+  const int base = chunk * ITERS * heads_per_iter;
   P lo[ITERS], hi[ITERS];
   T* dst[ITERS];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int64_t h = base + static_cast<int64_t>(it) * heads_per_iter + hl;
+    const int h = base + it * heads_per_iter + hl;
     dst[it] = nullptr;
     if (h < total) {
       const bool first = h < a.t0.heads;
@@ -126,7 +139,7 @@ template <typename T, typename TT, bool NEOX>
 __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
   const int half = a.head_dim / 2;
   const int64_t total_heads = a.t0.heads + a.t1.heads;
-  const int64_t pairs = a.tokens * total_heads * half;
+  const int64_t pairs = a.total_tokens * total_heads * half;
   for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < pairs;
        g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t i = g % half;
@@ -163,13 +176,14 @@ constexpr int64_t kWavesPerLaunch = int64_t(1) << 24;  // keeps grid work-items 
 template <typename T, typename TT, bool NEOX, int ITERS>
 hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   const int64_t heads_per_wave = ITERS * (kWave / per_unit);
-  d.chunks = ceil_div(d.t0.heads + d.t1.heads, heads_per_wave);
-  const int64_t waves = d.tokens * d.chunks;
-  for (int64_t first = 0; first < waves; first += kWavesPerLaunch) {
+  d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads, heads_per_wave));
+  d.pu_shift = (per_unit & (per_unit - 1)) == 0 ? __builtin_ctzll(per_unit) : -1;
+  const int64_t tokens_per_launch = std::max<int64_t>(1, kWavesPerLaunch / d.chunks);
+  for (int64_t first = 0; first < d.total_tokens; first += tokens_per_launch) {
     RopeDev part = d;
-    part.wave0 = first;
-    const int64_t count = std::min(kWavesPerLaunch, waves - first);
-    const dim3 grid(static_cast<unsigned>(ceil_div(count, kWavesPerBlock)));
+    part.token0 = static_cast<int>(first);
+    part.tokens = static_cast<int>(std::min(tokens_per_launch, d.total_tokens - first));
+    const dim3 grid(static_cast<unsigned>(ceil_div(int64_t(part.tokens) * d.chunks, kWavesPerBlock)));
     hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kWavesPerBlock>), grid,
                        dim3(kWave * kWavesPerBlock), 0, stream, part);
     const hipError_t err = hipGetLastError();
@@ -193,8 +207,8 @@ hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
 
 template <typename T, typename TT>
 hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
-  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, 1, a.batch * a.seq, a.seq,
-            static_cast<int>(a.head_dim), a.st};
+  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, 0, 1, static_cast<int>(a.seq),
+            static_cast<int>(a.head_dim), -1, a.st, a.batch * a.seq};
   if (a.vector_ok) {
     constexpr int E = 16 / sizeof(T);
     const int64_t unit = a.neox ? a.head_dim / 2 : a.head_dim;
@@ -202,7 +216,7 @@ hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
     return a.neox ? run_iters<T, TT, true>(d, per_unit, stream)
                   : run_iters<T, TT, false>(d, per_unit, stream);
   }
-  const int64_t pairs = d.tokens * (a.t0.heads + a.t1.heads) * (a.head_dim / 2);
+  const int64_t pairs = d.total_tokens * (a.t0.heads + a.t1.heads) * (a.head_dim / 2);
   const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(pairs, 256), 1 << 16));
   if (a.neox) {
     hipLaunchKernelGGL((rope_scalar<T, TT, true>), dim3(blocks), dim3(256), 0, stream, d);

@@ -30,7 +30,7 @@ from torch import nn
 
 from ako_amd.ops.rmsnorm import rmsnorm, rmsnorm_residual
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
-from ako_amd.ops.rope import rope
+from ako_amd.ops.rope import rope, rope_qk
 from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
 from ako_amd.ops.swiglu import swiglu
 
@@ -219,8 +219,13 @@ class Attention(nn.Module):
         q = self.q_proj(x).view(batch, seq_len, cfg.n_heads, cfg.head_dim)
         k = self.k_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
         v = self.v_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
-        q = _rope(self.backend, q, cos, sin, cfg.rope_style, self.kernel_override)
-        k = _rope(self.backend, k, cos, sin, cfg.rope_style, self.kernel_override)
+        if self.backend == "ako" and not (self.kernel_override or {}).get("rope"):
+            # One dispatched op (a single launch on the HIP path) for both tensors.
+            q, k = rope_qk(q, k, cos, sin, cfg.rope_style,
+                           kernel=(self.kernel_override or {}).get("rope_qk"))
+        else:
+            q = _rope(self.backend, q, cos, sin, cfg.rope_style, self.kernel_override)
+            k = _rope(self.backend, k, cos, sin, cfg.rope_style, self.kernel_override)
         if isinstance(kv_cache, StaticKVCache):
             kh, vh, mask, causal = kv_cache.update(layer_idx, k, v)
             if self.repeats > 1:

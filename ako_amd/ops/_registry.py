@@ -12,6 +12,11 @@ kernel                      backend            priority  registered when
 ``*_hip``                   ``hip``            5         unless ``AKO_HIP_DISABLE=1``
 ==========================  =================  ========  ===============
 
+One operation is added to the reference's four: ``rope_qk`` (query and key
+rotated by the same tables). Its reference is ``rope_qk_ref`` (two
+``rope_ref`` calls, ``ako/ops/rope_ref.py:110-118``); its HIP candidate
+rotates both tensors in one launch.
+
 The reference kernel has the highest priority, so with autotuning off (or on
 a CPU tensor) the safe unfused path is the default and the HIP kernels have
 to win a gated benchmark to be used. If the HIP library cannot be loaded
@@ -53,13 +58,14 @@ def _hip_entries() -> list[tuple[str, str, object]]:
         logger.info("HIP kernel library not loadable and no GPU present; HIP candidates skipped")
         return []
     from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
-    from ako_amd.ops.rope_hip import rope_hip
+    from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
     from ako_amd.ops.swiglu_hip import swiglu_hip
 
     return [
         ("rmsnorm", "rmsnorm_hip", rmsnorm_hip),
         ("rmsnorm_residual", "rmsnorm_residual_hip", rmsnorm_residual_hip),
         ("rope", "rope_hip", rope_hip),
+        ("rope_qk", "rope_qk_hip", rope_qk_hip),
         ("swiglu", "swiglu_hip", swiglu_hip),
     ]
 
@@ -81,7 +87,7 @@ def register_all(registry: KernelRegistry | None = None, *, force: bool = False)
         rope_compiled,
         swiglu_compiled,
     )
-    from ako_amd.ops.rope_ref import rope_ref
+    from ako_amd.ops.rope_ref import rope_qk_ref, rope_ref
     from ako_amd.ops.swiglu_ref import swiglu_ref
 
     entries: list[KernelEntry] = [
@@ -90,6 +96,7 @@ def register_all(registry: KernelRegistry | None = None, *, force: bool = False)
             ("rmsnorm", "rmsnorm_ref", rmsnorm_ref),
             ("rmsnorm_residual", "rmsnorm_residual_ref", rmsnorm_residual_ref),
             ("rope", "rope_ref", rope_ref),
+            ("rope_qk", "rope_qk_ref", rope_qk_ref),
             ("swiglu", "swiglu_ref", swiglu_ref),
         )
     ]

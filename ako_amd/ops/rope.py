@@ -39,8 +39,18 @@ def rope_qk(
     *,
     kernel: str | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """RoPE of a query/key pair (each tensor dispatched like :func:`rope`)."""
-    return rope(q, cos, sin, style, kernel=kernel), rope(k, cos, sin, style, kernel=kernel)
+    """RoPE of a query/key pair sharing the tables.
+
+    The reference applies :func:`rope` twice (``ako/ops/rope.py:45-58``);
+    here the pair is one dispatched operation, ``rope_qk``, whose HIP
+    candidate rotates both tensors in a single launch. The outputs are the
+    same as two :func:`rope` calls.
+    """
+    register_all()
+    fn = get_selector().select(
+        "rope_qk", q, k, cos, sin, forced=kernel, extra_key=style, call_kwargs={"style": style}
+    )
+    return fn(q, k, cos, sin, style)
 
 
 __all__ = ["build_rope_tables", "rope", "rope_qk"]

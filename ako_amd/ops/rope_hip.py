@@ -51,7 +51,7 @@ def rope_hip(
     xv = _head_view(x)
     c, s, st = _table_stride(_table(cos, index), _table(sin, index))
     batch, seq, heads, head_dim = x.shape
-    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    y = torch.empty_like(x) if x.is_contiguous() else torch.empty(x.shape, dtype=x.dtype, device=x.device)
     status = call(
         index, lib().ako_rope_fwd,
         xv.data_ptr(), c.data_ptr(), s.data_ptr(), y.data_ptr(),
@@ -66,8 +66,8 @@ def rope_hip(
     return y
 
 
-def _strides(t: torch.Tensor) -> ctypes.Array:
-    return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+_addressof = ctypes.addressof
+_I64x12 = ctypes.c_int64 * 12
 
 
 def rope_qk_hip(
@@ -86,13 +86,17 @@ def rope_qk_hip(
     qv, kv = _head_view(q), _head_view(k)
     c, s, st = _table_stride(_table(cos, index), _table(sin, index))
     batch, seq, q_heads, head_dim = q.shape
-    q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    q_out = torch.empty_like(q) if q.is_contiguous() else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    k_out = torch.empty_like(k) if k.is_contiguous() else torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    qs, ks, qos, kos = qv.stride(), kv.stride(), q_out.stride(), k_out.stride()
+    strides = _I64x12(qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
+                      qos[0], qos[1], qos[2], kos[0], kos[1], kos[2])
+    base = _addressof(strides)
     status = call(
         index, lib().ako_rope_qk_fwd,
         qv.data_ptr(), kv.data_ptr(), c.data_ptr(), s.data_ptr(),
         q_out.data_ptr(), k_out.data_ptr(), batch, seq, q_heads, k.shape[2], head_dim,
-        _strides(qv), _strides(kv), _strides(q_out), _strides(k_out),
+        base, base + 24, base + 48, base + 72,
         st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
         raw_stream(index),
     )

@@ -154,7 +154,8 @@ def test_selection_result_to_dict(tmp_path) -> None:
 
 def test_register_all_covers_every_op_with_safe_defaults() -> None:
     reg = register_all(KernelRegistry())
-    assert reg.list_ops() == ["rmsnorm", "rmsnorm_residual", "rope", "swiglu"]
+    # The reference's four operations, plus the one-launch query/key pair.
+    assert reg.list_ops() == ["rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"]
     for op in reg.list_ops():
         assert reg.default(op).backend == "pytorch"
         pytorch = [k for k in reg.list_kernels(op) if k.backend == "pytorch"]
@@ -169,7 +170,7 @@ def test_register_all_hip_candidates_and_opt_out(monkeypatch) -> None:
 
     reg = register_all(KernelRegistry())
     if _native.is_available():
-        for op in ("rmsnorm", "rmsnorm_residual", "rope", "swiglu"):
+        for op in ("rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"):
             hip = [k for k in reg.list_kernels(op) if k.backend == "hip"]
             assert [k.kernel_name for k in hip] == [f"{op}_hip"] and hip[0].priority == 5
     monkeypatch.setenv("AKO_HIP_DISABLE", "1")
