@@ -105,6 +105,12 @@ int ako_set_tuning(int op, int key, int value) {
         ako::g_rms_tuning.lds_reserve = value;
         return AKO_OK;
       }
+      if (key == 5) {
+        if (value > 2) return fail(AKO_ERR_INVALID_ARGUMENT, "row order must be 0, 1 or 2");
+        ako::g_rms_tuning.row_order = value;
+        return AKO_OK;
+      }
+      if (key == 6) { ako::g_rms_tuning.xcd_chunk = value; return AKO_OK; }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

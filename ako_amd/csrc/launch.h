@@ -19,6 +19,8 @@ struct RmsTuning {
   int vecs_per_thread = 0;  // key 2
   int force_stream = 0;     // key 3: 1 = always use the two-pass kernel
   int lds_reserve = 0;      // key 4: bytes of LDS reserved per workgroup (caps rows in flight per CU)
+  int row_order = 0;        // key 5: 1 = rows in block order, 2 = XCD-blocked order
+  int xcd_chunk = 0;        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
 };
 struct RopeTuning {
   int tokens_per_block = 0;  // key 1: waves (one token each) per workgroup

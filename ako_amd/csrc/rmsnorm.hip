@@ -13,7 +13,8 @@
 //   floats of LDS. Small rows pack RPB rows into one workgroup (the decode
 //   shapes: 1 or 32 rows). A lane issues every load of a group of packets
 //   before consuming any of them, so its memory latency is paid once per
-//   group instead of once per packet.
+//   group instead of once per packet. Wide rows are handed to the 8 XCDs in
+//   runs of consecutive rows (block_order) rather than row by row.
 //
 // rmsnorm_stream - any width, any alignment (E = 1 scalar packets when the
 //   rows are not 16-byte aligned). One 256-lane workgroup per row, two passes
@@ -53,11 +54,29 @@ struct WeightPacket {
   __device__ __forceinline__ float operator[](int e) const { return to_f32(part[e / kPer].e[e % kPer]); }
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
+// XCD b % 8). block_order hands each XCD runs of `chunk` consecutive blocks:
+// workgroup b = 8 i + x takes block c * 8 chunk + x * chunk + j for
+// i = c * chunk + j, so the XCDs walk 8 separate runs instead of interleaving
+// block by block. chunk <= 1 is the identity; the last, partial round of runs
+// is split evenly the same way and the n % 8 trailing blocks keep their own
+// index, which keeps the map a bijection on [0, n).
+__device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, unsigned chunk) {
+  const unsigned q = n / 8;
+  if (chunk <= 1 || b >= 8 * q) return b;
+  const unsigned x = b % 8, i = b / 8;
+  const unsigned full = q / chunk;
+  const unsigned c = i / chunk, j = i % chunk;
+  if (c < full) return c * 8 * chunk + x * chunk + j;
+  const unsigned rest = q - full * chunk;
+  return full * 8 * chunk + x * rest + (i - full * chunk);
+}
+
 template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     T* __restrict__ y, T* __restrict__ rout, int64_t rows, int hidden, int64_t sx, int64_t sr,
-    int64_t sy, int64_t srout, float inv_h, float eps) {
+    int64_t sy, int64_t srout, float inv_h, float eps, unsigned xcd_chunk) {
   constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per packet
   constexpr int TPR = kWave * WPR;                     // lanes per row
   // Packets are processed in groups: every load of a group is issued before
@@ -76,7 +95,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   const int row_in_block = wave / WPR;
   const int wave_in_row = wave - row_in_block * WPR;
   const int t = wave_in_row * kWave + lane;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + row_in_block;
+  const int64_t row = static_cast<int64_t>(block_order(blockIdx.x, gridDim.x, xcd_chunk)) * RPB + row_in_block;
   const bool active = row < rows;
   const int nvec = hidden / E;
   const int tail = hidden - nvec * E;
@@ -299,6 +318,8 @@ RegShape pick_shape(int64_t nvec, bool residual) {
   return s;
 }
 
+constexpr unsigned kXcdChunk = 8;
+
 template <typename T, typename W, int WPR, int VPT, bool RES>
 hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
@@ -307,15 +328,26 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   // A residual row of >= 32 KiB per tensor keeps 4 x 32 KiB in flight; two
   // such rows per CU exceed the CU's share of its XCD's L2 (4 MiB / 32 CUs),
   // so an LDS reservation above half the CU's 160 KiB limits those launches to
-  // one 16-wavefront workgroup per CU (measured +2-3% at 16384 x 16384).
+  // one 16-wavefront workgroup per CU (measured +1-3% at 16384 x 16384).
   unsigned lds = static_cast<unsigned>(g_rms_tuning.lds_reserve);
   if (lds == 0 && RES && WPR == 16 && a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024)
     lds = 82 * 1024;
+  // Default: rows of >= 16 KiB go to the XCDs in runs of 8 consecutive rows
+  // (once the launch holds 8 such runs); narrower rows keep block order.
+  // Medians of 5 cold runs on MI355X, 16384 rows, fp16/bf16, against block
+  // order: +1% at 16 KiB rows, +4% (plain) and +8-10% (residual) at 32 KiB
+  // rows, -1-2% at 8 KiB rows; whole-grid runs (chunk = n / 8) lose up to 12%
+  // at 8 KiB rows.
+  const bool wide = a.hidden * static_cast<int64_t>(sizeof(T)) >= 16 * 1024;
+  unsigned xcd_chunk = wide && grid.x >= 8 * kXcdChunk ? kXcdChunk : 1;
+  if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
+  if (g_rms_tuning.row_order == 2)
+    xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
   hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid, block, lds,
                      stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                      static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                      a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
-                     1.0f / static_cast<float>(a.hidden), a.eps);
+                     1.0f / static_cast<float>(a.hidden), a.eps, xcd_chunk);
   return hipGetLastError();
 }
 

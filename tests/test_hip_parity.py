@@ -163,6 +163,37 @@ def test_rmsnorm_every_register_shape() -> None:
             _native.set_tuning(0, key, 0)
 
 
+@pytest.mark.parametrize("rows", [127, 128, 1000, 2051])
+def test_rmsnorm_xcd_row_orders_cover_every_row(rows: int) -> None:
+    """Every row order maps workgroups onto rows one to one.
+
+    Row counts straddle the 128-workgroup threshold of the default chunked
+    order, and 1000 / 2051 leave partial runs and trailing blocks. Rows are
+    independent, so any order must give bit-identical outputs to block order.
+    """
+    from ako_amd import _native
+
+    x = grandn((rows, 2048), torch.float16, 30)
+    r = grandn((rows, 2048), torch.float16, 31)
+    w = grandn((2048,), torch.float16, 32, scale=0.1, shift=1.0)
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype="float16")
+    try:
+        _native.set_tuning(0, 5, 1)
+        base_y, base_s = rmsnorm_residual_hip(x, r, w)
+        base_p = rmsnorm_hip(x, w)
+        np.testing.assert_array_equal(to_np(base_s), es)
+        assert_oracle(ey, to_np(base_y), torch.float16)
+        for order, chunk in ((0, 0), (2, 0), (2, 1), (2, 3), (2, 16), (2, 100000)):
+            _native.set_tuning(0, 5, order)
+            _native.set_tuning(0, 6, chunk)
+            y, s = rmsnorm_residual_hip(x, r, w)
+            assert torch.equal(y, base_y) and torch.equal(s, base_s), (order, chunk)
+            assert torch.equal(rmsnorm_hip(x, w), base_p), (order, chunk)
+    finally:
+        for key in (5, 6):
+            _native.set_tuning(0, key, 0)
+
+
 def test_rmsnorm_empty_and_errors() -> None:
     w = torch.ones(64, device=DEV, dtype=torch.float16)
     empty = torch.empty(0, 64, device=DEV, dtype=torch.float16)
