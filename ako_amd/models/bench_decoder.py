@@ -6,7 +6,8 @@ RMSNorm / residual RMSNorm / RoPE / SwiGLU go through the ``ako_amd``
 dispatcher (``backend="ako"``) or the unfused eager references
 (``backend="torch"``). Reported per backend: prefill ms, decode ms (all 128
 steps and per step), wall clock around a synchronised region, plus the
-generated tokens so the two backends can be compared. Each backend is also
+generated tokens so the two backends can be compared. Prefill is the median of
+20 passes after 3 untimed ones; decode the median of 3 full 128-step runs. Each backend is also
 run with every decode step replayed from a HIP graph (``GraphedGreedy``),
 which removes the per-launch host cost that dominates batch-1 decoding.
 
@@ -35,7 +36,8 @@ def _timed(fn) -> tuple[Any, float]:
 
 
 def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3,
-                device: str = "cuda", seed: int = 0, graphed: bool = True) -> dict[str, Any]:
+                device: str = "cuda", seed: int = 0, graphed: bool = True, prefill_warmup: int = 3,
+                prefill_repeats: int = 20) -> dict[str, Any]:
     cfg = config5()
     cfg.max_seq_len = prompt_len + decode_steps
     model = build_lm(cfg, backend=backend, device=device, dtype=torch.float16, seed=seed)
@@ -44,10 +46,19 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
 
     with torch.no_grad():
         model.generate_greedy(prompt, decode_steps)  # warmup, incl. first-sight kernel selection
-        prefill_ms, decode_ms, tokens = [], [], None
+        # Prefill on its own: a few untimed passes, then the median of many
+        # (one pass is ~2 ms, so a handful of samples is at the mercy of clock
+        # ramp-up after the host-bound decode loop).
+        prefill_ms = []
+        for i in range(prefill_warmup + prefill_repeats):
+            cache = model.stack.new_kv_cache(prompt_len + decode_steps)
+            _, t_pre = _timed(lambda: model.logits_last(prompt, cache).argmax(-1, keepdim=True))
+            if i >= prefill_warmup:
+                prefill_ms.append(t_pre)
+        decode_ms, tokens = [], None
         for _ in range(repeats):
             cache = model.stack.new_kv_cache(prompt_len + decode_steps)
-            nxt, t_pre = _timed(lambda: model.logits_last(prompt, cache).argmax(-1, keepdim=True))
+            nxt = model.logits_last(prompt, cache).argmax(-1, keepdim=True)
 
             def decode(nxt=nxt, cache=cache):
                 out = [nxt]
@@ -57,7 +68,6 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
                 return torch.cat(out, dim=1)
 
             tokens, t_dec = _timed(decode)
-            prefill_ms.append(t_pre)
             decode_ms.append(t_dec)
         graphed_ms, graphed_tokens = [], None
         if graphed:
@@ -79,6 +89,7 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
     return {
         "backend": backend,
         "prefill_ms": round(prefill, 3),
+        "prefill_samples": len(prefill_ms),
         "decode_ms": round(dec, 3),
         "decode_ms_per_step": round(dec / max(decode_steps - 1, 1), 4),
         "prompt_len": prompt_len,
