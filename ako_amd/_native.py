@@ -57,6 +57,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
          _ptr, _i64, _int, _int, _int, _ptr],
     ),
+    "ako_rope_qk_cache_fwd": (
+        _int,
+        [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64,
+         _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _int, _int, _int, _ptr],
+    ),
     "ako_swiglu_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _int, _ptr]),
     "ako_set_tuning": (_int, [_int, _int, _int]),
 }

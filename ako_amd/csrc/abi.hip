@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -192,18 +193,41 @@ struct RopeTensorIn {
   void* y;
   int64_t heads;
   const int64_t* xs;  // strides b, s, h
-  const int64_t* ys;
+  const int64_t* ys;  // strides b, s (cache tensors: slot), h
+  bool at_pos;        // output rows are cache slots (*pos + s), cache_len of them
 };
 
-// Extent, in elements, of a [batch, seq, heads, head_dim] view with the given
+// Extent, in elements, of a [n0, n1, n2, head_dim] view with the given
 // strides (last dimension contiguous): offset of the last element + 1.
-int64_t extent4(int64_t b, int64_t s, int64_t h, int64_t d, const int64_t* st) {
-  return (b - 1) * st[0] + (s - 1) * st[1] + (h - 1) * st[2] + d;
+int64_t extent4(int64_t n0, int64_t n1, int64_t n2, int64_t d, const int64_t* st) {
+  return (n0 - 1) * st[0] + (n1 - 1) * st[1] + (n2 - 1) * st[2] + d;
 }
 
+// True when distinct (i0, i1, i2, e) of a [n0, n1, n2, head_dim] view address
+// distinct elements: taken in order of increasing stride, every dimension of
+// more than one index must step past everything the smaller ones span. Any
+// nesting order passes (heads-major cache slabs as well as token-major views).
+bool distinct_rows(int64_t n0, int64_t n1, int64_t n2, int64_t head_dim, const int64_t* st) {
+  struct Dim { int64_t stride, count; } dims[3] = {{st[0], n0}, {st[1], n1}, {st[2], n2}};
+  for (int i = 0; i < 3; ++i)
+    for (int j = i + 1; j < 3; ++j)
+      if (dims[j].stride < dims[i].stride) std::swap(dims[i], dims[j]);
+  __int128 reach = head_dim;
+  for (const Dim& d : dims) {
+    if (d.count <= 1) continue;
+    if (d.stride < reach) return false;
+    reach += static_cast<__int128>(d.stride) * (d.count - 1);
+  }
+  return true;
+}
+
+// Cache mode: pos != nullptr. Tensors with at_pos write rows 0..cache_len-1
+// (selected on the device by *pos + s); the tables must hold table_rows >=
+// cache_len rows. Tensor index 2 is copied, not rotated.
 int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos, const void* sin,
                 int64_t batch, int64_t seq, int64_t head_dim, int64_t st, int dtype,
-                int table_dtype, int style, void* stream) {
+                int table_dtype, int style, void* stream, const int64_t* pos = nullptr,
+                int64_t cache_len = 0, int64_t table_rows = 0) {
   if (!valid_dtype(dtype) || !valid_dtype(table_dtype))
     return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code (x %d, table %d)", fn, dtype, table_dtype);
   if (style != AKO_ROPE_NEOX && style != AKO_ROPE_INTERLEAVED)
@@ -211,6 +235,12 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
   if (batch < 0 || seq < 0 || head_dim < 0)
     return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
   if (head_dim % 2 != 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: head_dim must be even, got %lld", fn, (long long)head_dim);
+  const bool cache = pos != nullptr;
+  if (cache && (cache_len <= 0 || cache_len > kMaxInt))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: cache_len must be in [1, 2^31-1], got %lld", fn, (long long)cache_len);
+  if (cache && table_rows < cache_len)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: the tables hold %lld rows, fewer than cache_len %lld", fn,
+                (long long)table_rows, (long long)cache_len);
   int64_t total_heads = 0;
   for (int i = 0; i < nt; ++i) {
     if (ts[i].heads < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative head count", fn);
@@ -221,26 +251,33 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
   if (batch > kMaxInt / seq || total_heads > kMaxInt)
     return fail(AKO_ERR_INVALID_ARGUMENT, "%s: batch*seq and the head count must stay below 2^31", fn);
   if (!cos || !sin) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null table pointer", fn);
-  if (st < head_dim / 2 && seq > 1) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: table row stride %lld < head_dim/2", fn, (long long)st);
+  const int64_t tab_rows = cache ? cache_len : seq;  // rows the kernel may read
+  if (st < head_dim / 2 && tab_rows > 1) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: table row stride %lld < head_dim/2", fn, (long long)st);
   const int eb = ako::dtype_bytes(dtype);
   const int tb = ako::dtype_bytes(table_dtype);
-  const Span cos_span = span_2d(cos, seq, head_dim / 2, st, tb);
-  const Span sin_span = span_2d(sin, seq, head_dim / 2, st, tb);
-  Span out_spans[2], in_spans[2];
+  const Span cos_span = span_2d(cos, tab_rows, head_dim / 2, st, tb);
+  const Span sin_span = span_2d(sin, tab_rows, head_dim / 2, st, tb);
+  Span out_spans[3], in_spans[3];
   for (int i = 0; i < nt; ++i) {
     const RopeTensorIn& t = ts[i];
     if (t.heads == 0) continue;
     if (!t.x || !t.y || !t.xs || !t.ys) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
     for (int k = 0; k < 3; ++k)
       if (t.xs[k] < 0 || t.ys[k] < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative stride", fn);
-    // Distinct output elements must not alias: require the usual nesting.
-    if ((t.heads > 1 && t.ys[2] < head_dim) || (seq > 1 && t.ys[1] < t.heads * head_dim) ||
-        (batch > 1 && t.ys[0] < seq * t.heads * head_dim))
+    const int64_t out_rows = t.at_pos ? cache_len : seq;
+    // Distinct output elements must not alias.
+    if (!distinct_rows(batch, out_rows, t.heads, head_dim, t.ys))
       return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output strides make rows overlap", fn);
     in_spans[i] = Span{reinterpret_cast<uintptr_t>(t.x),
                        reinterpret_cast<uintptr_t>(t.x) + static_cast<uintptr_t>(extent4(batch, seq, t.heads, head_dim, t.xs)) * eb};
     out_spans[i] = Span{reinterpret_cast<uintptr_t>(t.y),
-                        reinterpret_cast<uintptr_t>(t.y) + static_cast<uintptr_t>(extent4(batch, seq, t.heads, head_dim, t.ys)) * eb};
+                        reinterpret_cast<uintptr_t>(t.y) + static_cast<uintptr_t>(extent4(batch, out_rows, t.heads, head_dim, t.ys)) * eb};
+  }
+  if (cache) {
+    const Span pos_span{reinterpret_cast<uintptr_t>(pos), reinterpret_cast<uintptr_t>(pos) + sizeof(int64_t)};
+    for (int i = 0; i < nt; ++i)
+      if (ts[i].heads != 0 && overlap(out_spans[i], pos_span))
+        return fail(AKO_ERR_INVALID_ARGUMENT, "%s: an output overlaps pos", fn);
   }
   for (int i = 0; i < nt; ++i) {
     if (ts[i].heads == 0) continue;
@@ -251,7 +288,7 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
       if (overlap(out_spans[i], in_spans[k]))
         return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output overlaps an input", fn);
       if (k != i && overlap(out_spans[i], out_spans[k]))
-        return fail(AKO_ERR_INVALID_ARGUMENT, "%s: the two outputs overlap", fn);
+        return fail(AKO_ERR_INVALID_ARGUMENT, "%s: two outputs overlap", fn);
     }
   }
 
@@ -277,7 +314,13 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
   };
   a.t0 = conv(ts[0]);
   a.t1 = nt > 1 ? conv(ts[1]) : none;
-  if (a.t0.heads == 0) { a.t0 = a.t1; a.t1 = none; }
+  a.t2 = nt > 2 ? conv(ts[2]) : none;
+  // Without a cache the roles of t0 and t1 are the same; a launch with only
+  // the second tensor moves it first. In cache mode the roles differ (t0 is
+  // written at s, t1 at the cache slot) and an empty t0 simply has no heads.
+  if (!cache && a.t0.heads == 0) { a.t0 = a.t1; a.t1 = none; }
+  a.pos = pos;
+  a.cache_len = cache ? cache_len : 0;
   a.cos = cos;
   a.sin = sin;
   a.batch = batch;
@@ -300,7 +343,7 @@ int ako_rope_fwd(const void* x, const void* cos_table, const void* sin_table, vo
                  int style, void* stream) {
   const int64_t xs[3] = {x_stride_b, x_stride_s, x_stride_h};
   const int64_t ys[3] = {y_stride_b, y_stride_s, y_stride_h};
-  const RopeTensorIn t{x, y, heads, xs, ys};
+  const RopeTensorIn t{x, y, heads, xs, ys, false};
   return rope_common("ako_rope_fwd", &t, 1, cos_table, sin_table, batch, seq, head_dim,
                      table_row_stride, dtype, table_dtype, style, stream);
 }
@@ -311,10 +354,30 @@ int ako_rope_qk_fwd(const void* q, const void* k, const void* cos_table, const v
                     const int64_t* k_strides, const int64_t* q_out_strides,
                     const int64_t* k_out_strides, int64_t table_row_stride, int dtype,
                     int table_dtype, int style, void* stream) {
-  const RopeTensorIn ts[2] = {{q, q_out, q_heads, q_strides, q_out_strides},
-                              {k, k_out, k_heads, k_strides, k_out_strides}};
+  const RopeTensorIn ts[2] = {{q, q_out, q_heads, q_strides, q_out_strides, false},
+                              {k, k_out, k_heads, k_strides, k_out_strides, false}};
   return rope_common("ako_rope_qk_fwd", ts, 2, cos_table, sin_table, batch, seq, head_dim,
                      table_row_stride, dtype, table_dtype, style, stream);
+}
+
+int ako_rope_qk_cache_fwd(const void* q, const void* k, const void* v, const void* cos_table,
+                          const void* sin_table, void* q_out, void* k_cache, void* v_cache,
+                          const int64_t* pos, int64_t batch, int64_t seq, int64_t q_heads,
+                          int64_t kv_heads, int64_t head_dim, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides,
+                          const int64_t* q_out_strides, const int64_t* cache_strides,
+                          int64_t cache_len, int64_t table_rows, int64_t table_row_stride,
+                          int dtype, int table_dtype, int style, void* stream) {
+  const char* fn = "ako_rope_qk_cache_fwd";
+  if (!pos) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null pos pointer", fn);
+  if ((v == nullptr) != (v_cache == nullptr))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: v and v_cache must both be given or both be null", fn);
+  const int64_t v_heads = v ? kv_heads : 0;
+  const RopeTensorIn ts[3] = {{q, q_out, q_heads, q_strides, q_out_strides, false},
+                              {k, k_cache, kv_heads, k_strides, cache_strides, true},
+                              {v, v_cache, v_heads, v_strides, cache_strides, true}};
+  return rope_common(fn, ts, 3, cos_table, sin_table, batch, seq, head_dim, table_row_stride, dtype,
+                     table_dtype, style, stream, pos, cache_len, table_rows);
 }
 
 // ----------------------------------------------------------------- SwiGLU --

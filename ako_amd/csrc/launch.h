@@ -61,6 +61,13 @@ struct RopeTensorArgs {
 struct RopeArgs {
   RopeTensorArgs t0;
   RopeTensorArgs t1;  // heads == 0 when only one tensor is rotated
+  // KV-cache mode (pos != nullptr): token s sits at position p = *pos + s; the
+  // tables are read at row p, t1's output row is slot p (rotated keys into the
+  // cache) and t2 is copied unrotated to slot p of its output (values). Tokens
+  // with p outside [0, cache_len) are not written.
+  RopeTensorArgs t2;
+  const int64_t* pos;
+  int64_t cache_len;
   const void* cos;
   const void* sin;
   int64_t batch, seq, head_dim;

@@ -17,6 +17,12 @@
 //
 // rope_scalar - any head_dim, any alignment: one lane per rotated pair.
 //
+// Both kernels have a KV-cache mode (CACHE): the position of token s is read
+// on the device (*pos + s), the tables are read at that row, q is rotated to
+// its output, k is rotated into slot *pos + s of the key cache and v is copied
+// into the same slot of the value cache, all in the one launch. A captured
+// decode step can then be replayed while *pos advances.
+//
 // Numerics follow ako/ops/rope_ref.py:73-107: a' = a*c - b*n and
 // b' = a*n + b*c in fp32 with each product rounded separately (the library is
 // built with -ffp-contract=off), then rounded to the storage dtype.
@@ -39,7 +45,9 @@ struct RopeTensorDev {
 };
 
 struct RopeDev {
-  RopeTensorDev t0, t1;
+  RopeTensorDev t0, t1, t2;  // t2: copied, not rotated (KV-cache mode only)
+  const int64_t* pos;        // KV-cache mode: device-side position of token s = 0
+  int64_t cache_len;
   const void* cos;
   const void* sin;
   int token0;        // first token of this launch (launches split at token boundaries)
@@ -52,7 +60,7 @@ struct RopeDev {
   int64_t total_tokens;  // batch * seq (scalar kernel)
 };
 
-template <typename T, typename TT, bool NEOX, int ITERS, int TPB>
+template <typename T, typename TT, bool NEOX, int ITERS, int TPB, bool CACHE>
 __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   constexpr int E = 16 / static_cast<int>(sizeof(T));
   constexpr int NT = NEOX ? E : E / 2;  // table values per lane
@@ -84,24 +92,36 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
 
   const int b = token / a.seq;
   const int s = token - b * a.seq;
+  // Row of the tables and, in KV-cache mode, the cache slot of this token.
+  int p = s;
+  if constexpr (CACHE) {
+    const int64_t pp = *a.pos + s;
+    if (pp < 0 || pp >= a.cache_len) return;  // out of the cache: nothing is written
+    p = static_cast<int>(pp);
+  }
   float c[NT], n[NT];
-  load_f32<TT, NT>(static_cast<const TT*>(a.cos) + s * a.st + j * NT, c);
-  load_f32<TT, NT>(static_cast<const TT*>(a.sin) + s * a.st + j * NT, n);
+  load_f32<TT, NT>(static_cast<const TT*>(a.cos) + p * a.st + j * NT, c);
+  load_f32<TT, NT>(static_cast<const TT*>(a.sin) + p * a.st + j * NT, n);
 
-  const int total = static_cast<int>(a.t0.heads + a.t1.heads);
+  const int h01 = static_cast<int>(a.t0.heads + a.t1.heads);
+  const int total = h01 + (CACHE ? static_cast<int>(a.t2.heads) : 0);
   const int base = chunk * ITERS * heads_per_iter;
   P lo[ITERS], hi[ITERS];
   T* dst[ITERS];
+  [[maybe_unused]] bool copy[ITERS];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int h = base + it * heads_per_iter + hl;
     dst[it] = nullptr;
     if (h < total) {
       const bool first = h < a.t0.heads;
-      const RopeTensorDev& tt = first ? a.t0 : a.t1;
-      const int64_t hh = first ? h : h - a.t0.heads;
+      const bool third = CACHE && h >= h01;
+      const RopeTensorDev& tt = first ? a.t0 : (third ? a.t2 : a.t1);
+      const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
+      const int64_t srow = (CACHE && !first) ? p : s;
       const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh + j * E;
-      dst[it] = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh + j * E;
+      dst[it] = static_cast<T*>(tt.y) + b * tt.syb + srow * tt.sys + hh * tt.syh + j * E;
+      if constexpr (CACHE) copy[it] = third;
       lo[it] = load_pack<T, E, true>(src);
       if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
     }
@@ -109,6 +129,13 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     if (dst[it] == nullptr) continue;
+    if constexpr (CACHE) {
+      if (copy[it]) {
+        store_pack<T, E, true>(dst[it], lo[it]);
+        if constexpr (NEOX) store_pack<T, E, true>(dst[it] + half, hi[it]);
+        continue;
+      }
+    }
     if constexpr (NEOX) {
       P olo, ohi;
 #pragma unroll
@@ -135,11 +162,13 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
 }
 
 // One lane per rotated pair; a grid-stride loop so any size fits one launch.
-template <typename T, typename TT, bool NEOX>
+template <typename T, typename TT, bool NEOX, bool CACHE>
 __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
   const int half = a.head_dim / 2;
-  const int64_t total_heads = a.t0.heads + a.t1.heads;
+  const int64_t h01 = a.t0.heads + a.t1.heads;
+  const int64_t total_heads = h01 + (CACHE ? a.t2.heads : 0);
   const int64_t pairs = a.total_tokens * total_heads * half;
+  const int64_t p0 = CACHE ? *a.pos : 0;
   for (int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < pairs;
        g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t i = g % half;
@@ -148,15 +177,24 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
     const int64_t token = th / total_heads;
     const int64_t b = token / a.seq;
     const int64_t s = token - b * a.seq;
+    const int64_t p = CACHE ? p0 + s : s;
+    if (CACHE && (p < 0 || p >= a.cache_len)) continue;
     const bool first = h < a.t0.heads;
-    const RopeTensorDev& tt = first ? a.t0 : a.t1;
-    const int64_t hh = first ? h : h - a.t0.heads;
+    const bool third = CACHE && h >= h01;
+    const RopeTensorDev& tt = first ? a.t0 : (third ? a.t2 : a.t1);
+    const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
+    const int64_t srow = (CACHE && !first) ? p : s;
     const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh;
-    T* dst = static_cast<T*>(tt.y) + b * tt.syb + s * tt.sys + hh * tt.syh;
+    T* dst = static_cast<T*>(tt.y) + b * tt.syb + srow * tt.sys + hh * tt.syh;
     const int64_t ia = NEOX ? i : 2 * i;
     const int64_t ib = NEOX ? i + half : 2 * i + 1;
-    const float c = to_f32(static_cast<const TT*>(a.cos)[s * a.st + i]);
-    const float n = to_f32(static_cast<const TT*>(a.sin)[s * a.st + i]);
+    if (third) {
+      dst[ia] = src[ia];
+      dst[ib] = src[ib];
+      continue;
+    }
+    const float c = to_f32(static_cast<const TT*>(a.cos)[p * a.st + i]);
+    const float n = to_f32(static_cast<const TT*>(a.sin)[p * a.st + i]);
     const float x0 = to_f32(src[ia]);
     const float x1 = to_f32(src[ib]);
     dst[ia] = from_f32<T>(x0 * c - x1 * n);
@@ -173,10 +211,10 @@ RopeTensorDev to_dev(const RopeTensorArgs& t) {
 constexpr int kWavesPerBlock = 4;
 constexpr int64_t kWavesPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
 
-template <typename T, typename TT, bool NEOX, int ITERS>
+template <typename T, typename TT, bool NEOX, int ITERS, bool CACHE>
 hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   const int64_t heads_per_wave = ITERS * (kWave / per_unit);
-  d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads, heads_per_wave));
+  d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads + (CACHE ? d.t2.heads : 0), heads_per_wave));
   d.pu_shift = (per_unit & (per_unit - 1)) == 0 ? __builtin_ctzll(per_unit) : -1;
   const int64_t tokens_per_launch = std::max<int64_t>(1, kWavesPerLaunch / d.chunks);
   for (int64_t first = 0; first < d.total_tokens; first += tokens_per_launch) {
@@ -184,7 +222,7 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
     part.token0 = static_cast<int>(first);
     part.tokens = static_cast<int>(std::min(tokens_per_launch, d.total_tokens - first));
     const dim3 grid(static_cast<unsigned>(ceil_div(int64_t(part.tokens) * d.chunks, kWavesPerBlock)));
-    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kWavesPerBlock>), grid,
+    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kWavesPerBlock, CACHE>), grid,
                        dim3(kWave * kWavesPerBlock), 0, stream, part);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -199,16 +237,17 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
 template <typename T, typename TT, bool NEOX>
 hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
   const int iters = g_rope_tuning.iters > 0 ? g_rope_tuning.iters : 1;
-  if (iters <= 1) return run_vec<T, TT, NEOX, 1>(d, per_unit, stream);
-  if (iters <= 2) return run_vec<T, TT, NEOX, 2>(d, per_unit, stream);
-  if (iters <= 4) return run_vec<T, TT, NEOX, 4>(d, per_unit, stream);
-  return run_vec<T, TT, NEOX, 8>(d, per_unit, stream);
+  if (d.pos != nullptr) return run_vec<T, TT, NEOX, 1, true>(d, per_unit, stream);
+  if (iters <= 1) return run_vec<T, TT, NEOX, 1, false>(d, per_unit, stream);
+  if (iters <= 2) return run_vec<T, TT, NEOX, 2, false>(d, per_unit, stream);
+  if (iters <= 4) return run_vec<T, TT, NEOX, 4, false>(d, per_unit, stream);
+  return run_vec<T, TT, NEOX, 8, false>(d, per_unit, stream);
 }
 
 template <typename T, typename TT>
 hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
-  RopeDev d{to_dev(a.t0), to_dev(a.t1), a.cos, a.sin, 0, 0, 1, static_cast<int>(a.seq),
-            static_cast<int>(a.head_dim), -1, a.st, a.batch * a.seq};
+  RopeDev d{to_dev(a.t0), to_dev(a.t1), to_dev(a.t2), a.pos, a.cache_len, a.cos, a.sin, 0, 0, 1,
+            static_cast<int>(a.seq), static_cast<int>(a.head_dim), -1, a.st, a.batch * a.seq};
   if (a.vector_ok) {
     constexpr int E = 16 / sizeof(T);
     const int64_t unit = a.neox ? a.head_dim / 2 : a.head_dim;
@@ -216,12 +255,16 @@ hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
     return a.neox ? run_iters<T, TT, true>(d, per_unit, stream)
                   : run_iters<T, TT, false>(d, per_unit, stream);
   }
-  const int64_t pairs = d.total_tokens * (a.t0.heads + a.t1.heads) * (a.head_dim / 2);
+  const int64_t heads = a.t0.heads + a.t1.heads + (a.pos != nullptr ? a.t2.heads : 0);
+  const int64_t pairs = d.total_tokens * heads * (a.head_dim / 2);
   const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(pairs, 256), 1 << 16));
-  if (a.neox) {
-    hipLaunchKernelGGL((rope_scalar<T, TT, true>), dim3(blocks), dim3(256), 0, stream, d);
+  const dim3 grid(blocks), block(256);
+  if (a.pos != nullptr) {
+    if (a.neox) hipLaunchKernelGGL((rope_scalar<T, TT, true, true>), grid, block, 0, stream, d);
+    else hipLaunchKernelGGL((rope_scalar<T, TT, false, true>), grid, block, 0, stream, d);
   } else {
-    hipLaunchKernelGGL((rope_scalar<T, TT, false>), dim3(blocks), dim3(256), 0, stream, d);
+    if (a.neox) hipLaunchKernelGGL((rope_scalar<T, TT, true, false>), grid, block, 0, stream, d);
+    else hipLaunchKernelGGL((rope_scalar<T, TT, false, false>), grid, block, 0, stream, d);
   }
   return hipGetLastError();
 }

@@ -30,7 +30,7 @@ from torch import nn
 
 from ako_amd.ops.rmsnorm import rmsnorm, rmsnorm_residual
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
-from ako_amd.ops.rope import rope, rope_qk
+from ako_amd.ops.rope import rope, rope_qk, rope_qk_cache
 from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
 from ako_amd.ops.swiglu import swiglu
 
@@ -196,6 +196,14 @@ def _rope(backend: Backend, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tenso
     return rope(x, cos, sin, style, kernel=(override or {}).get("rope"))
 
 
+def _fused_cache_rope(backend: Backend, override: KernelOverride | None) -> bool:
+    """Whether a static-cache decode step rotates q/k and appends k/v to the
+    cache in one call (``rope_qk_cache``) instead of RoPE plus two copies.
+    Forcing a ``rope`` or ``rope_qk`` kernel keeps the unfused path."""
+    o = override or {}
+    return backend == "ako" and not o.get("rope") and not o.get("rope_qk")
+
+
 class Attention(nn.Module):
     """Grouped-query attention with RoPE and SDPA."""
 
@@ -219,6 +227,17 @@ class Attention(nn.Module):
         q = self.q_proj(x).view(batch, seq_len, cfg.n_heads, cfg.head_dim)
         k = self.k_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
         v = self.v_proj(x).view(batch, seq_len, cfg.n_kv_heads, cfg.head_dim)
+        if (isinstance(kv_cache, StaticKVCache) and seq_len == 1
+                and _fused_cache_rope(self.backend, self.kernel_override)):
+            # cos/sin are the full tables here; the position is read on the device.
+            q = rope_qk_cache(q, k, v, cos, sin, kv_cache.pos, kv_cache.k[layer_idx],
+                              kv_cache.v[layer_idx], cfg.rope_style)
+            kh, vh = kv_cache.k[layer_idx], kv_cache.v[layer_idx]
+            if self.repeats > 1:
+                kh = kh.repeat_interleave(self.repeats, dim=1)
+                vh = vh.repeat_interleave(self.repeats, dim=1)
+            attn = F.scaled_dot_product_attention(q.transpose(1, 2), kh, vh, attn_mask=kv_cache.mask)
+            return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
         if self.backend == "ako" and not (self.kernel_override or {}).get("rope"):
             # One dispatched op (a single launch on the HIP path) for both tensors.
             q, k = rope_qk(q, k, cos, sin, cfg.rope_style,
@@ -324,7 +343,10 @@ class DecoderStack(nn.Module):
         static_step = isinstance(kv_cache, StaticKVCache) and x.shape[1] == 1
         if static_step:
             full = self.rope_tables(self.config.max_seq_len, device=x.device)
-            cos, sin = kv_cache.rope_rows(*full)
+            if _fused_cache_rope(self.backend, self.kernel_override):
+                cos, sin = full  # the fused cache RoPE picks row pos itself
+            else:
+                cos, sin = kv_cache.rope_rows(*full)
             kv_cache.begin_step()
         else:
             offset = kv_cache.length if kv_cache is not None else 0

@@ -9,7 +9,8 @@ positionally or as the ``style=`` keyword, as the selector passes it
 tables may be fp32, fp16 or bf16 regardless of x's dtype.
 
 ``rope_qk_hip`` rotates a query/key pair in a single launch; the reference's
-``rope_qk`` issues two (``ako/ops/rope.py:45-58``).
+``rope_qk`` issues two (``ako/ops/rope.py:45-58``). ``rope_qk_cache_hip`` also
+writes the rotated keys and the values into a KV cache in that launch.
 """
 
 from __future__ import annotations
@@ -103,3 +104,81 @@ def rope_qk_hip(
     if status:
         _native.check(status, "rope_qk_hip")
     return q_out, k_out
+
+
+_I64x15 = ctypes.c_int64 * 15
+
+
+def rope_qk_cache_hip(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor | None,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor | None,
+    style: str = "neox",
+) -> torch.Tensor:
+    """One launch: rotated q out, rotated k and unrotated v into slot ``pos[0] + s``
+    of the heads-major ``(batch, kv_heads, cache_len, head_dim)`` caches.
+
+    ``pos`` stays on the device and is read by the kernel, so the launch can
+    be captured in a HIP graph while the position advances between replays.
+    Tokens whose slot falls outside the cache are not written (the host
+    cannot see ``pos`` without a synchronisation); callers keep
+    ``pos + seq <= cache_len``.
+    """
+    index = gpu_index(q, "rope_qk_cache_hip")
+    if q.dim() != 4 or k.dim() != 4 or k_cache.dim() != 4:
+        raise ValueError("rope_qk_cache_hip: q, k and k_cache must be 4-D")
+    batch, seq, q_heads, head_dim = q.shape
+    kv_heads = k.shape[2]
+    cache_len = k_cache.shape[2]
+    if style not in _native.ROPE_STYLE_CODES:
+        raise ValueError(f"Unknown RoPE style {style!r}")
+    if tuple(k.shape) != (batch, seq, kv_heads, head_dim) or k.dtype != q.dtype:
+        raise ValueError(f"rope_qk_cache_hip: k {tuple(k.shape)} {k.dtype} does not match q {tuple(q.shape)} {q.dtype}")
+    if tuple(k_cache.shape) != (batch, kv_heads, cache_len, head_dim) or k_cache.dtype != q.dtype:
+        raise ValueError(f"rope_qk_cache_hip: k_cache {tuple(k_cache.shape)} {k_cache.dtype} is not "
+                         f"(batch, kv_heads, cache_len, head_dim) of {q.dtype}")
+    if (v is None) != (v_cache is None):
+        raise ValueError("rope_qk_cache_hip: v and v_cache must both be given or both be None")
+    if v is not None and (tuple(v.shape) != tuple(k.shape) or v.dtype != q.dtype
+                          or tuple(v_cache.shape) != tuple(k_cache.shape) or v_cache.dtype != q.dtype
+                          or v_cache.stride() != k_cache.stride()):
+        raise ValueError("rope_qk_cache_hip: v / v_cache must match k / k_cache (shapes, dtype, strides)")
+    if cos.dim() != 2 or cos.shape[1] != head_dim // 2 or sin.shape != cos.shape:
+        raise ValueError(f"rope_qk_cache_hip: tables must be (positions, {head_dim // 2}), got {tuple(cos.shape)}")
+    if pos.dtype != torch.int64 or pos.numel() < 1:
+        raise ValueError("rope_qk_cache_hip: pos must be an int64 tensor holding the position")
+    for name, t in (("k", k), ("k_cache", k_cache), ("pos", pos)) + (
+            (("v", v), ("v_cache", v_cache)) if v is not None else ()):
+        if not t.is_cuda or t.get_device() != index:
+            raise ValueError(f"rope_qk_cache_hip: {name} must be on the device of q")
+    if k_cache.stride(-1) != 1 or (v_cache is not None and v_cache.stride(-1) != 1):
+        raise ValueError("rope_qk_cache_hip: cache rows must be contiguous in head_dim")
+    dt = dtype_code(q.dtype, "rope_qk_cache_hip")
+    qv, kv = _head_view(q), _head_view(k)
+    vv = _head_view(v) if v is not None else None
+    c, s, st = _table_stride(_table(cos, index), _table(sin, index))
+    q_out = torch.empty_like(q) if q.is_contiguous() else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    qs, ks, qos = qv.stride(), kv.stride(), q_out.stride()
+    vs = vv.stride() if vv is not None else (0, 0, 0, 0)
+    cs = k_cache.stride()
+    strides = _I64x15(qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                      qos[0], qos[1], qos[2], cs[0], cs[2], cs[1])
+    base = _addressof(strides)
+    status = call(
+        index, lib().ako_rope_qk_cache_fwd,
+        qv.data_ptr(), kv.data_ptr(), vv.data_ptr() if vv is not None else None,
+        c.data_ptr(), s.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr() if v_cache is not None else None, pos.data_ptr(),
+        batch, seq, q_heads, kv_heads, head_dim,
+        base, base + 24, base + 48, base + 72, base + 96,
+        cache_len, c.shape[0], st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
+        raw_stream(index),
+    )
+    if status:
+        _native.check(status, "rope_qk_cache_hip")
+    return q_out

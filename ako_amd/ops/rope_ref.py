@@ -85,3 +85,35 @@ def rope_qk_ref(
     q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
 ) -> tuple[torch.Tensor, torch.Tensor]:
     return rope_ref(q, cos, sin, style), rope_ref(k, cos, sin, style)
+
+
+def rope_qk_cache_ref(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor | None,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor | None,
+    style: str = "neox",
+) -> torch.Tensor:
+    """RoPE of q and k at positions ``pos[0] + s`` with the keys (and values)
+    appended to a heads-major cache, as the unfused composition the
+    reference's decoder runs: ``rope(q)``, ``rope(k)`` and the cache append
+    (``ako/models/decoder.py:173-177``).
+
+    ``cos``/``sin`` are the full ``(max_positions, head_dim/2)`` tables,
+    ``pos`` a one-element int64 tensor, ``k_cache``/``v_cache`` are
+    ``(batch, kv_heads, cache_len, head_dim)``. Returns the rotated q; the
+    caches are written in place.
+    """
+    seq = q.shape[1]
+    slots = pos.reshape(-1)[:1] + torch.arange(seq, device=pos.device)
+    c = cos.index_select(0, slots)
+    s = sin.index_select(0, slots)
+    q_out = rope_ref(q, c, s, style)
+    k_cache.index_copy_(2, slots, rope_ref(k, c, s, style).transpose(1, 2))
+    if v is not None:
+        v_cache.index_copy_(2, slots, v.transpose(1, 2))
+    return q_out

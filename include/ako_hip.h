@@ -125,6 +125,34 @@ int ako_rope_qk_fwd(const void* q, const void* k, const void* cos_table, const v
                     int dtype, int table_dtype, int style, void* stream);
 
 /*
+ * RoPE of a query/key pair with the rotated keys (and the values, copied)
+ * written straight into a KV cache, in ONE launch. This is the fused consumer
+ * the reference's decoder performs as rope(q), rope(k) and a cache append
+ * (ako/models/decoder.py:173-177, KVCache.update at :84-93).
+ *   position of token s:  p = *pos + s   (pos: one int64 in device memory,
+ *                                         read by the kernel, so a captured
+ *                                         launch follows a moving position)
+ *   q_out[b, s, h]      = rope(q[b, s, h], row p of cos/sin)
+ *   k_cache[b, h, slot p] = rope(k[b, s, h], row p)
+ *   v_cache[b, h, slot p] = v[b, s, h]          (v and v_cache may both be NULL)
+ * q/k/v/q_out strides are (batch, seq, head); cache_strides (batch, slot,
+ * head) are shared by both caches, in elements. The tables hold table_rows
+ * >= cache_len rows. Tokens whose p falls outside [0, cache_len) are not
+ * written at all (q_out included); keeping *pos + seq <= cache_len is the
+ * caller's contract, as it is for the reference's cache.
+ */
+int ako_rope_qk_cache_fwd(const void* q, const void* k, const void* v,
+                          const void* cos_table, const void* sin_table,
+                          void* q_out, void* k_cache, void* v_cache, const int64_t* pos,
+                          int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads,
+                          int64_t head_dim,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* v_strides, const int64_t* q_out_strides,
+                          const int64_t* cache_strides,
+                          int64_t cache_len, int64_t table_rows, int64_t table_row_stride,
+                          int dtype, int table_dtype, int style, void* stream);
+
+/*
  * SwiGLU activation: y = to_dtype( silu(gate) * up ), silu(g) = g / (1 + e^-g),
  * over [rows, n] with row strides in elements.
  * Replaces swiglu_triton + _swiglu_kernel_impl

@@ -137,6 +137,38 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, style: str = "neox", *
     return round_to(out, dtype)
 
 
+def rope_qk_cache(q: np.ndarray, k: np.ndarray, v: np.ndarray | None, cos: np.ndarray,
+                  sin: np.ndarray, pos: int, k_cache: np.ndarray, v_cache: np.ndarray | None,
+                  style: str = "neox", *, dtype: str = "float32",
+                  table_dtype: str = "float32") -> tuple[np.ndarray, np.ndarray, np.ndarray | None]:
+    """The reference decoder's per-layer ``rope(q)``, ``rope(k)`` and cache
+    append (decoder.py:173-177, KVCache.update at :84-93), with the cache laid
+    out heads-major ``(batch, kv_heads, cache_len, head_dim)`` and the new
+    tokens at slots ``pos .. pos + seq - 1``; the tables are the full
+    ``(positions, head_dim/2)`` ones, read at the same rows.
+
+    Returns ``(q_rotated, new_k_cache, new_v_cache)``; the inputs are not
+    modified. Tokens whose slot falls outside the cache are dropped (q rows
+    included, which are returned as zeros), matching the kernel contract.
+    """
+    seq = q.shape[1]
+    cache_len = k_cache.shape[2]
+    keep = [s for s in range(seq) if 0 <= pos + s < cache_len]
+    q_out = np.zeros_like(q)
+    new_k = k_cache.copy()
+    new_v = None if v_cache is None else v_cache.copy()
+    if not keep:
+        return q_out, new_k, new_v
+    rows = np.array([pos + s for s in keep])
+    c, sn = cos[rows], sin[rows]
+    q_out[:, keep] = rope(q[:, keep], c, sn, style, dtype=dtype, table_dtype=table_dtype)
+    k_rot = rope(k[:, keep], c, sn, style, dtype=dtype, table_dtype=table_dtype)
+    new_k[:, :, rows] = k_rot.transpose(0, 2, 1, 3)
+    if v is not None:
+        new_v[:, :, rows] = v[:, keep].transpose(0, 2, 1, 3)
+    return q_out, new_k, new_v
+
+
 # -- SwiGLU -------------------------------------------------------------------------
 
 

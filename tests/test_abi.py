@@ -36,7 +36,7 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_abi() -> None:
     names = declared_functions()
     assert {"ako_rmsnorm_fwd", "ako_rmsnorm_residual_fwd", "ako_rope_fwd", "ako_rope_qk_fwd",
-            "ako_swiglu_fwd", "ako_last_error", "ako_abi_version"} <= set(names)
+            "ako_rope_qk_cache_fwd", "ako_swiglu_fwd", "ako_last_error", "ako_abi_version"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib) -> None:
@@ -117,6 +117,29 @@ def test_rope_qk_validation(lib) -> None:
     assert "two outputs overlap" in _native.last_error()
     assert f(A, B, C, D, E, 0x600000, 0, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == OK
     assert f(A, None, C, D, E, 0x600000, 1, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == INVALID
+
+
+def test_rope_qk_cache_validation(lib) -> None:
+    """KV-cache RoPE: argument checks that run before any launch."""
+    f = lib.ako_rope_qk_cache_fwd
+    tok = (ctypes.c_int64 * 3)(16, 16, 8)          # q/k/v/q_out: (batch, seq, head)
+    heads_major = (ctypes.c_int64 * 3)(256, 8, 128)  # cache (batch, slot, head) of [1, 2, 16, 8]
+    Q, K, V, COS, SIN, QO, KC, VC, POS = (0x100000 * i for i in range(1, 10))
+
+    def call(*, v=V, vc=VC, pos=POS, kc=KC, cache=heads_major, cache_len=16, rows=16, batch=1):
+        return f(Q, K, v, COS, SIN, QO, kc, vc, pos, batch, 1, 2, 2, 8, tok, tok, tok, tok, cache,
+                 cache_len, rows, 4, F16, F32, 0, None)
+
+    assert call(batch=0) == OK
+    assert call(pos=None) == INVALID and "pos" in _native.last_error()
+    assert call(vc=None) == INVALID and "v_cache" in _native.last_error()
+    assert call(rows=15) == INVALID and "fewer than cache_len" in _native.last_error()
+    assert call(cache_len=0) == INVALID
+    assert call(vc=KC + 64) == INVALID and "two outputs overlap" in _native.last_error()
+    slots_overlap = (ctypes.c_int64 * 3)(256, 4, 128)
+    assert call(cache=slots_overlap) == INVALID and "overlap" in _native.last_error()
+    assert call(kc=POS - 16) == INVALID and "pos" in _native.last_error()
+    assert call(kc=COS) == INVALID and "table" in _native.last_error()
 
 
 def test_swiglu_validation(lib) -> None:

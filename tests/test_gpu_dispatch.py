@@ -11,7 +11,7 @@ from ako_amd.dispatcher.registry import KernelRegistry
 from ako_amd.dispatcher.selector import KernelSelector
 from ako_amd.ops._registry import register_all
 from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
-from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
 from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
 from ako_amd.ops.swiglu_hip import swiglu_hip
@@ -94,6 +94,42 @@ def test_hip_graph_replays_match_eager() -> None:
         torch.cuda.synchronize()
         for want, got in zip(eager, captured):
             assert torch.equal(want, got), f"replay {i} differs"
+
+
+def test_cache_rope_graph_follows_the_device_position() -> None:
+    """rope_qk_cache captured once with the position advanced inside the graph:
+    replay n writes slot start + n, exactly as the eager call at that position."""
+    hq, hkv, d, cache_len, start = 8, 2, 128, 24, 5
+    q = _rand(1, 1, hq, d, dtype=torch.float16, seed=7)
+    k = _rand(1, 1, hkv, d, dtype=torch.float16, seed=8)
+    v = _rand(1, 1, hkv, d, dtype=torch.float16, seed=9)
+    cos, sin = build_rope_tables(cache_len, d, device=DEV)
+    kc = torch.zeros(1, hkv, cache_len, d, device=DEV, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    pos = torch.full((1,), start, dtype=torch.int64, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        rope_qk_cache_hip(q, k, v, cos, sin, pos, kc, vc)  # warm-up, rewritten by replay 0
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        q_out = rope_qk_cache_hip(q, k, v, cos, sin, pos, kc, vc)
+        pos.add_(1)
+    kc_eager, vc_eager = torch.zeros_like(kc), torch.zeros_like(vc)
+    for n in range(6):
+        for t, seed in ((q, 20 + n), (k, 30 + n), (v, 40 + n)):  # new token, eager work between replays
+            t.copy_(_rand(*t.shape, dtype=t.dtype, seed=seed))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        at = torch.tensor([start + n], dtype=torch.int64, device=DEV)
+        want_q = rope_qk_cache_hip(q, k, v, cos, sin, at, kc_eager, vc_eager)
+        assert torch.equal(q_out, want_q), n
+        assert int(pos.item()) == start + n + 1
+    assert torch.equal(kc, kc_eager) and torch.equal(vc, vc_eager)
+    assert not kc[:, :, :start].any() and not kc[:, :, start + 6:].any()
 
 
 def test_decoder_backends_agree_on_gpu() -> None:

@@ -21,7 +21,7 @@ import torch
 
 from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
-from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
 from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
 from ako_amd.ops.swiglu_hip import swiglu_hip
 from ako_amd.ops.swiglu_ref import swiglu_ref
@@ -264,6 +264,60 @@ def test_rope_strided_views(style: str) -> None:
     c2, s2 = full[0][10:26], full[1][10:26]
     assert_oracle(oracle.rope(to_np(q), to_np(c2), to_np(s2), style, dtype="bfloat16"),
                   to_np(rope_hip(q, c2, s2, style)), torch.bfloat16)
+
+
+CACHE_CASES = [
+    (1, 1, 32, 32, 128, 511, 640),  # configs[4] decode step: MHA, slot 511 of 640
+    (2, 5, 8, 2, 128, 3, 16),       # GQA, several tokens at once
+    (1, 4, 4, 4, 6, 0, 8),          # head_dim 6: the scalar kernel
+    (1, 3, 2, 2, 64, 6, 8),         # the last token's slot (8) is past the cache: dropped
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+@pytest.mark.parametrize("batch,seq,hq,hkv,d,pos,cache_len", CACHE_CASES)
+def test_rope_qk_cache(batch, seq, hq, hkv, d, pos, cache_len, style: str, dtype) -> None:
+    """q rotated out, k rotated and v copied into heads-major cache slots pos + s."""
+    q = grandn((batch, seq, hq, d), dtype, 40)
+    k = grandn((batch, seq, hkv, d), dtype, 41)
+    v = grandn((batch, seq, hkv, d), dtype, 42)
+    kc = grandn((batch, hkv, cache_len, d), dtype, 43)
+    vc = grandn((batch, hkv, cache_len, d), dtype, 44)
+    cos, sin = build_rope_tables(cache_len, d, device=DEV)
+    pos_t = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    eq, ek, ev = oracle.rope_qk_cache(to_np(q), to_np(k), to_np(v), to_np(cos), to_np(sin), pos,
+                                      to_np(kc), to_np(vc), style, dtype=NAMES[dtype])
+    q_out = rope_qk_cache_hip(q, k, v, cos, sin, pos_t, kc, vc, style)
+    kept = [s for s in range(seq) if pos + s < cache_len]
+    untouched = [t for t in range(cache_len) if not pos <= t < pos + len(kept)]
+    assert_oracle(eq[:, kept], to_np(q_out[:, kept]), dtype)
+    assert_oracle(ek, to_np(kc), dtype)
+    np.testing.assert_array_equal(to_np(kc)[:, :, untouched], ek[:, :, untouched])
+    np.testing.assert_array_equal(to_np(vc), ev)
+    # The same rotation as the one-launch pair kernel on the same table rows, bit for bit.
+    n = len(kept)
+    qo, ko = rope_qk_hip(q[:, :n], k[:, :n], cos[pos:pos + n], sin[pos:pos + n], style)
+    assert torch.equal(q_out[:, :n], qo)
+    assert torch.equal(kc[:, :, pos:pos + n], ko.transpose(1, 2))
+
+
+def test_rope_qk_cache_without_values_and_rejects() -> None:
+    q = grandn((1, 1, 4, 128), torch.float16, 45)
+    k = grandn((1, 1, 2, 128), torch.float16, 46)
+    kc = torch.zeros(1, 2, 32, 128, device=DEV, dtype=torch.float16)
+    cos, sin = build_rope_tables(32, 128, device=DEV)
+    pos = torch.tensor([7], dtype=torch.int64, device=DEV)
+    q_out = rope_qk_cache_hip(q, k, None, cos, sin, pos, kc, None)
+    qo, ko = rope_qk_hip(q, k, cos[7:8], sin[7:8])
+    assert torch.equal(q_out, qo) and torch.equal(kc[:, :, 7:8], ko.transpose(1, 2))
+    assert not kc[:, :, :7].any() and not kc[:, :, 8:].any()
+    with pytest.raises(ValueError, match="int64"):
+        rope_qk_cache_hip(q, k, None, cos, sin, pos.int(), kc, None)
+    with pytest.raises(ValueError, match="fewer than cache_len"):
+        rope_qk_cache_hip(q, k, None, cos[:16], sin[:16], pos, kc, None)
+    with pytest.raises(ValueError, match="both"):
+        rope_qk_cache_hip(q, k, k, cos, sin, pos, kc, None)
 
 
 def test_rope_every_iteration_count() -> None:

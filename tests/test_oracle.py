@@ -184,6 +184,82 @@ def test_rope_rejects_bad_input() -> None:
         ops.rope(np.zeros((1, 4, 1, 8), np.float32), cos, sin, "unknown-style")
 
 
+def _brute_rotate(vec: np.ndarray, position: int, style: str, base: float = 10000.0) -> np.ndarray:
+    """Float64 rotation of one head vector at ``position``, element by element."""
+    d = vec.shape[0]
+    half = d // 2
+    out = np.empty(d, np.float64)
+    for i in range(half):
+        theta = position * base ** (-2.0 * i / d)
+        c, s = math.cos(theta), math.sin(theta)
+        ia, ib = (i, i + half) if style == "neox" else (2 * i, 2 * i + 1)
+        a, b = float(vec[ia]), float(vec[ib])
+        out[ia] = a * c - b * s
+        out[ib] = a * s + b * c
+    return out
+
+
+def _check_cache_against_brute(fn, style: str) -> None:
+    rng = np.random.default_rng(21)
+    batch, seq, q_heads, kv_heads, d, cache_len, pos = 2, 3, 3, 2, 8, 9, 4
+    q = rng.standard_normal((batch, seq, q_heads, d)).astype(np.float32)
+    k = rng.standard_normal((batch, seq, kv_heads, d)).astype(np.float32)
+    v = rng.standard_normal((batch, seq, kv_heads, d)).astype(np.float32)
+    k_cache = rng.standard_normal((batch, kv_heads, cache_len, d)).astype(np.float32)
+    v_cache = rng.standard_normal((batch, kv_heads, cache_len, d)).astype(np.float32)
+    cos, sin = ops.rope_tables(cache_len, d)
+    q_out, new_k, new_v = fn(q, k, v, cos, sin, pos, k_cache, v_cache, style)
+    for b in range(batch):
+        for s in range(seq):
+            for h in range(q_heads):
+                np.testing.assert_allclose(q_out[b, s, h], _brute_rotate(q[b, s, h], pos + s, style),
+                                           atol=2e-6, rtol=0)
+            for h in range(kv_heads):
+                np.testing.assert_allclose(new_k[b, h, pos + s], _brute_rotate(k[b, s, h], pos + s, style),
+                                           atol=2e-6, rtol=0)
+                np.testing.assert_array_equal(new_v[b, h, pos + s], v[b, s, h])
+    untouched = [t for t in range(cache_len) if not pos <= t < pos + seq]
+    np.testing.assert_array_equal(new_k[:, :, untouched], k_cache[:, :, untouched])
+    np.testing.assert_array_equal(new_v[:, :, untouched], v_cache[:, :, untouched])
+
+
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+def test_rope_qk_cache_matches_brute_force(style: str) -> None:
+    """Slot placement, table row and rotation of the cache composition, against
+    an element-by-element float64 loop over math.cos / math.sin."""
+    _check_cache_against_brute(ops.rope_qk_cache, style)
+
+
+def test_rope_qk_cache_drops_out_of_range_tokens() -> None:
+    rng = np.random.default_rng(22)
+    q = rng.standard_normal((1, 4, 1, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 4, 1, 8)).astype(np.float32)
+    kc = np.zeros((1, 1, 6, 8), np.float32)
+    cos, sin = ops.rope_tables(6, 8)
+    q_out, new_k, new_v = ops.rope_qk_cache(q, k, None, cos, sin, 4, kc, None)
+    assert new_v is None
+    assert np.any(q_out[:, :2]) and not np.any(q_out[:, 2:])   # slots 4, 5 kept; 6, 7 dropped
+    assert np.any(new_k[:, :, 4:]) and not np.any(new_k[:, :, :4])
+
+
+def test_rope_qk_cache_planted_mistakes_are_caught() -> None:
+    """Writing at slot s instead of pos + s, or reading table row s, must fail."""
+
+    def wrong_slot(q, k, v, cos, sin, pos, k_cache, v_cache, style):
+        q_out, _, _ = ops.rope_qk_cache(q, k, v, cos, sin, pos, k_cache, v_cache, style)
+        _, new_k, new_v = ops.rope_qk_cache(q, k, v, cos, sin, 0, k_cache, v_cache, style)
+        return q_out, new_k, new_v
+
+    def wrong_row(q, k, v, cos, sin, pos, k_cache, v_cache, style):
+        shifted_c = np.roll(cos, pos, axis=0)
+        shifted_s = np.roll(sin, pos, axis=0)
+        return ops.rope_qk_cache(q, k, v, shifted_c, shifted_s, pos, k_cache, v_cache, style)
+
+    for planted in (wrong_slot, wrong_row):
+        with pytest.raises(AssertionError):
+            _check_cache_against_brute(planted, "neox")
+
+
 # -- SwiGLU ----------------------------------------------------------------------------
 
 
