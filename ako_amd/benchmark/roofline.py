@@ -49,6 +49,14 @@ def alg_bytes_rope(batch: int, seq: int, heads: int, head_dim: int, dtype: torch
     return 2 * batch * seq * heads * head_dim * elem_bytes(dtype) + 2 * seq * (head_dim // 2) * elem_bytes(table_dtype)
 
 
+def alg_bytes_rope_qk_cache(batch: int, seq: int, q_heads: int, kv_heads: int, head_dim: int,
+                            dtype: torch.dtype, table_dtype: torch.dtype, *, values: bool = True) -> int:
+    """q read and written, k read and written into the cache, v (when given)
+    read and copied into the cache, one table row pair per token."""
+    heads = q_heads + kv_heads + (kv_heads if values else 0)
+    return 2 * batch * seq * heads * head_dim * elem_bytes(dtype) + 2 * seq * (head_dim // 2) * elem_bytes(table_dtype)
+
+
 def alg_bytes_swiglu(rows: int, n: int, dtype: torch.dtype) -> int:
     return 3 * rows * n * elem_bytes(dtype)
 

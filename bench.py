@@ -73,7 +73,7 @@ def main() -> int:
     from ako_amd import _native
     from ako_amd.benchmark import roofline as rf
     from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
-    from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+    from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
     from ako_amd.ops.rope_ref import build_rope_tables
     from ako_amd.ops.swiglu_hip import swiglu_hip
 
@@ -154,6 +154,25 @@ def main() -> int:
                                   lambda k=ks[i], c=cos, sn=sin: rope_hip(k, c, sn, "neox")))
                     cells.append((f"rope_qk_{tag}_{b}x{s}", rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype),
                                   lambda q=qs[i], k=ks[i], c=cos, sn=sin: rope_qk_hip(q, k, c, sn, "neox")))
+        # configs[4] decode step, one layer: RoPE of q and k plus the KV-cache
+        # append, fused (one launch) and as the unfused sequence it replaces.
+        dtype = torch.float16
+        full_cos, full_sin = build_rope_tables(640, 128, device=dev)
+        q1, k1, v1 = rnd(1, 1, 32, 128, dtype=dtype), rnd(1, 1, 32, 128, dtype=dtype), rnd(1, 1, 32, 128, dtype=dtype)
+        kc, vc = rnd(1, 32, 640, 128, dtype=dtype), rnd(1, 32, 640, 128, dtype=dtype)
+        pos = torch.full((1,), 511, dtype=torch.long, device=dev)
+        cache_bytes = rf.alg_bytes_rope_qk_cache(1, 1, 32, 32, 128, dtype, torch.float32)
+
+        def unfused_cache_step():
+            c, sn = full_cos.index_select(0, pos), full_sin.index_select(0, pos)
+            qo, ko = rope_qk_hip(q1, k1, c, sn, "neox")
+            kc.index_copy_(2, pos, ko.transpose(1, 2))
+            vc.index_copy_(2, pos, v1.transpose(1, 2))
+            return qo
+
+        cells.append(("rope_qk_cache_fp16_1x1_q32_kv32_slot511of640", cache_bytes,
+                      lambda: rope_qk_cache_hip(q1, k1, v1, full_cos, full_sin, pos, kc, vc, "neox")))
+        cells.append(("rope_qk_then_index_copy_fp16_1x1_q32_kv32", cache_bytes, unfused_cache_step))
         for m in (16384, 4096, 256, 16, 1):
             dtype = torch.bfloat16
             nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)
