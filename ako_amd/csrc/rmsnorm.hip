@@ -126,11 +126,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
             v[g0 + k].e[e] = from_f32<T>(to_f32(v[g0 + k].e[e]) + to_f32(rv[k].e[e]));
           store_pack<T, E, NTS>(rout + row * srout + vi * E, v[g0 + k]);
         }
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const float f = to_f32(v[g0 + k].e[e]);
-          ss = __builtin_fmaf(f, f, ss);
-        }
+        ss = sumsq_add(v[g0 + k], ss);
       }
     }
   }
