@@ -23,7 +23,7 @@ struct RmsTuning {
   int xcd_chunk = 0;        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
 };
 struct RopeTuning {
-  int tokens_per_block = 0;  // key 1: waves (one token each) per workgroup
+  int tokens_per_block = 0;  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)
   int iters = 0;             // key 2: head chunks unrolled per loop trip
 };
 struct SwigluTuning {

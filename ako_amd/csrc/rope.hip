@@ -211,7 +211,7 @@ RopeTensorDev to_dev(const RopeTensorArgs& t) {
 constexpr int kWavesPerBlock = 4;
 constexpr int64_t kWavesPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
 
-template <typename T, typename TT, bool NEOX, int ITERS, bool CACHE>
+template <typename T, typename TT, bool NEOX, int ITERS, bool CACHE, int TPB = kWavesPerBlock>
 hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   const int64_t heads_per_wave = ITERS * (kWave / per_unit);
   d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads + (CACHE ? d.t2.heads : 0), heads_per_wave));
@@ -221,9 +221,9 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
     RopeDev part = d;
     part.token0 = static_cast<int>(first);
     part.tokens = static_cast<int>(std::min(tokens_per_launch, d.total_tokens - first));
-    const dim3 grid(static_cast<unsigned>(ceil_div(int64_t(part.tokens) * d.chunks, kWavesPerBlock)));
-    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, kWavesPerBlock, CACHE>), grid,
-                       dim3(kWave * kWavesPerBlock), 0, stream, part);
+    const dim3 grid(static_cast<unsigned>(ceil_div(int64_t(part.tokens) * d.chunks, TPB)));
+    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, TPB, CACHE>), grid, dim3(kWave * TPB), 0,
+                       stream, part);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -238,7 +238,15 @@ template <typename T, typename TT, bool NEOX>
 hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
   const int iters = g_rope_tuning.iters > 0 ? g_rope_tuning.iters : 1;
   if (d.pos != nullptr) return run_vec<T, TT, NEOX, 1, true>(d, per_unit, stream);
-  if (iters <= 1) return run_vec<T, TT, NEOX, 1, false>(d, per_unit, stream);
+  if (iters <= 1) {
+    switch (g_rope_tuning.tokens_per_block) {
+      case 1: return run_vec<T, TT, NEOX, 1, false, 1>(d, per_unit, stream);
+      case 2: return run_vec<T, TT, NEOX, 1, false, 2>(d, per_unit, stream);
+      case 8: return run_vec<T, TT, NEOX, 1, false, 8>(d, per_unit, stream);
+      case 16: return run_vec<T, TT, NEOX, 1, false, 16>(d, per_unit, stream);
+      default: return run_vec<T, TT, NEOX, 1, false>(d, per_unit, stream);
+    }
+  }
   if (iters <= 2) return run_vec<T, TT, NEOX, 2, false>(d, per_unit, stream);
   if (iters <= 4) return run_vec<T, TT, NEOX, 4, false>(d, per_unit, stream);
   return run_vec<T, TT, NEOX, 8, false>(d, per_unit, stream);
