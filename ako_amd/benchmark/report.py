@@ -25,6 +25,10 @@ class BenchmarkReport:
     results: list[dict[str, Any]] = field(default_factory=list)
     comparisons: list[dict[str, Any]] = field(default_factory=list)
     created_at: str = field(default_factory=lambda: datetime.now(timezone.utc).isoformat())
+    #: Optional rocprofv3 counter figures (``ako_amd.benchmark.rocprof.traffic``)
+    #: stored beside the timing rows; absent from the JSON when unset, so
+    #: reports keep the reference's layout.
+    counters: dict[str, Any] | None = None
 
     def add_result(self, result: BenchResult, **extra: Any) -> None:
         self.results.append({**result.to_dict(), **extra})
@@ -64,8 +68,20 @@ class BenchmarkReport:
         row.update(extra)
         self.comparisons.append(row)
 
+    def attach_counters(self, traffic_result: dict[str, Any]) -> None:
+        """Keep counter-measured HBM traffic next to the timings, and add
+        ``fetch_bytes`` / ``write_bytes`` / ``traffic_over_alg`` to every
+        comparison row whose ``cell`` names a measured kernel."""
+        self.counters = traffic_result
+        kernels = traffic_result.get("kernels", {})
+        for row in self.comparisons:
+            k = kernels.get(row.get("cell"))
+            if k is not None:
+                row.update(fetch_bytes=k["fetch_bytes"], write_bytes=k["write_bytes"],
+                           traffic_over_alg=k["traffic_over_alg"])
+
     def to_dict(self) -> dict[str, Any]:
-        return {
+        out = {
             "operation": self.operation,
             "gpu": self.device.device_name,
             "device": self.device.to_dict(),
@@ -73,6 +89,9 @@ class BenchmarkReport:
             "results": self.results,
             "comparisons": self.comparisons,
         }
+        if self.counters is not None:
+            out["counters"] = self.counters
+        return out
 
 
 def save_report(report: BenchmarkReport, path: str | Path) -> Path:

@@ -156,11 +156,19 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--title", default="rocprofv3 kernel statistics")
     ap.add_argument("--command", default="")
     ap.add_argument("--md", type=Path, required=True)
+    ap.add_argument("--json", type=Path, help="also write the figures as JSON (e.g. next to a BenchmarkReport)")
     args = ap.parse_args(argv)
     if args.stats:
-        args.md.write_text(stats_markdown(read_kernel_stats(args.stats), args.command, args.title))
+        rows = read_kernel_stats(args.stats)
+        args.md.write_text(stats_markdown(rows, args.command, args.title))
+        record: dict[str, Any] = {"kind": "kernel_stats", "title": args.title, "kernels": rows}
     else:
-        args.md.write_text(to_markdown(traffic(args.fetch, args.write, args.manifest), args.command))
+        result = traffic(args.fetch, args.write, args.manifest)
+        args.md.write_text(to_markdown(result, args.command))
+        record = {"kind": "hbm_traffic", **result}
+    if args.json:
+        args.json.parent.mkdir(parents=True, exist_ok=True)
+        args.json.write_text(json.dumps({**record, "command": args.command}, indent=2) + "\n")
     print(args.md.read_text())
     return 0
 

@@ -75,7 +75,22 @@ def cells(ops: set[str], device: torch.device) -> Iterator[tuple[str, list[int],
             yield "swiglu", [m, 14336], torch.bfloat16, (g, u), {}
 
 
-def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20) -> dict[str, Any]:
+def cell_name(op: str, shape: list[int], dtype: torch.dtype) -> str:
+    """The cell's name as the counter runs (``ako_amd.benchmark.counters``)
+    and ``bench.py`` spell it, so counter figures can be attached to rows."""
+    tag = {torch.float16: "fp16", torch.bfloat16: "bf16", torch.float32: "fp32"}[dtype]
+    if op in ("rmsnorm", "rmsnorm_residual"):
+        return f"{op}_{tag}_{shape[0]}x{shape[1]}"
+    if op == "rope":
+        which = "q" if shape[2] == 32 else "k"
+        return f"rope_{which}_{tag}_{shape[0]}x{shape[1]}x{shape[2]}x{shape[3]}"
+    if op == "rope_qk":
+        return f"rope_qk_{tag}_{shape[0]}x{shape[1]}"
+    return f"{op}_{tag}_{'x'.join(map(str, shape))}"
+
+
+def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
+        counters: dict[str, Any] | None = None) -> dict[str, Any]:
     device = torch.device("cuda", torch.cuda.current_device())
     info = get_device_info(device)
     registry = register_all(KernelRegistry())
@@ -92,6 +107,7 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20) -> 
         report.add_comparison(
             shape=shape,
             dtype=str(dtype).replace("torch.", ""),
+            cell=cell_name(op, shape, dtype),
             baseline_ms=result.baseline_ms or 0.0,
             baseline_kernel=f"{op}_ref",
             candidate_ms=lat.get(hip_name, float("nan")),
@@ -111,6 +127,8 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20) -> 
         del tensors
     out_dir.mkdir(parents=True, exist_ok=True)
     for op, report in reports.items():
+        if counters is not None:
+            report.attach_counters(counters)
         save_report(report, out_dir / f"selection_{op}.json")
     summary = {"cells": total, "hip_selected": wins, "hip_win_rate": round(wins / total, 4) if total else None,
                "gpu": info.device_name}
@@ -124,11 +142,15 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--ops", default="rmsnorm,rmsnorm_residual,rope,rope_qk,swiglu")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--repeats", type=int, default=20)
+    ap.add_argument("--counters", type=Path, default=None,
+                    help="HBM-traffic JSON from `python -m ako_amd.benchmark.rocprof ... --json` to attach")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("the selection sweep needs a GPU", file=sys.stderr)
         return 1
-    summary = run(args.out, set(args.ops.split(",")), warmup=args.warmup, repeats=args.repeats)
+    counters = json.loads(args.counters.read_text()) if args.counters else None
+    summary = run(args.out, set(args.ops.split(",")), warmup=args.warmup, repeats=args.repeats,
+                  counters=counters)
     print(json.dumps(summary), flush=True)
     return 0
 

@@ -3,6 +3,8 @@ graph capture fallbacks, regression diffs, roofline arithmetic."""
 
 from __future__ import annotations
 
+import json
+
 import random
 import statistics
 
@@ -26,7 +28,8 @@ from ako_amd.benchmark.report import BenchmarkReport
 from ako_amd.dispatcher.hardware import get_device_info
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
 from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
-from ako_amd.validation.regression import compare_reports
+from ako_amd.validation.regression import compare_bench_lines, compare_reports
+from ako_amd.validation import regression
 
 
 def test_bench_op_cpu_basics() -> None:
@@ -106,6 +109,47 @@ def test_report_and_regression_diff() -> None:
     assert compare_reports(slower, report.to_dict())
     other_dtype = {"comparisons": [dict(row, candidate_ms=0.4, dtype="bfloat16")]}
     assert compare_reports(other_dtype, report.to_dict()) == []
+
+
+def test_report_carries_counters_without_changing_its_layout() -> None:
+    report = BenchmarkReport(operation="rmsnorm", device=get_device_info("cpu"))
+    report.add_comparison(shape=[16384, 4096], baseline_ms=1.0, candidate_ms=0.05, max_error=0.0,
+                          selected_kernel="rmsnorm_hip", cell="rmsnorm_fp16_16384x4096")
+    plain = report.to_dict()
+    assert "counters" not in plain  # the reference's keys only, until counters are attached
+    traffic = {"reference": "reference_neg_fp16_1GiB", "fetch_factor": 2.0, "write_factor": 1.0,
+               "kernels": {"rmsnorm_fp16_16384x4096": {"alg_bytes": 268443648, "fetch_bytes": 134322434,
+                                                       "write_bytes": 134218794, "hbm_bytes_per_launch": 268541228,
+                                                       "traffic_over_alg": 1.0004}}}
+    report.attach_counters(traffic)
+    out = report.to_dict()
+    assert out["counters"]["fetch_factor"] == 2.0
+    assert out["comparisons"][0]["traffic_over_alg"] == 1.0004
+    assert set(plain) <= set(out)
+
+
+def _bench_line(value=6300.0, gbps=6000.0, graph_us=2.0, decode=0.78) -> dict:
+    return {"metric": "m", "value": value, "higher_is_better": True,
+            "per_kernel": [{"name": "rmsnorm_fp16_16384x4096", "gbps": gbps}],
+            "extras": [{"name": "rmsnorm_fp16_1x4096", "gbps": 3.6, "graph_us": graph_us}],
+            "decoder": {"ako": {"prefill_ms": 1.7, "decode_ms_per_step": 1.1,
+                                "graphed_decode_ms_per_step": decode}}}
+
+
+def test_bench_line_regression_diff(tmp_path) -> None:
+    base = _bench_line()
+    assert compare_bench_lines(_bench_line(), base) == []
+    assert compare_bench_lines(_bench_line(value=6350.0, gbps=6100.0, graph_us=1.9, decode=0.7), base) == []
+    warnings = compare_bench_lines(_bench_line(value=5000.0, gbps=5000.0, graph_us=3.0, decode=0.9), base)
+    assert len(warnings) == 4
+    assert any("graph_us" in w for w in warnings) and any("graphed_decode" in w for w in warnings)
+    assert compare_bench_lines({**_bench_line(), "metric": "other"}, base)[0].startswith("Different")
+    # The command line reads the last JSON line of each file and fails on a regression.
+    cur, old = tmp_path / "cur.json", tmp_path / "old.json"
+    old.write_text("[bench] log line\n" + json.dumps(base) + "\n")
+    cur.write_text(json.dumps(_bench_line(value=5000.0)) + "\n")
+    assert regression.main([str(cur), str(old)]) == 1
+    assert regression.main([str(old), str(old)]) == 0
 
 
 def test_graph_capture_is_a_noop_on_cpu() -> None:
