@@ -100,6 +100,54 @@ def traffic(fetch_csv: Path, write_csv: Path, manifest_path: Path) -> dict[str, 
     }
 
 
+def read_kernel_trace(path: Path) -> list[tuple[str, int, int]]:
+    """``(kernel name, start ns, end ns)`` rows of a ``*_kernel_trace.csv``, by start."""
+    with open(path, newline="") as fh:
+        rows = [(r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+                for r in csv.DictReader(fh)]
+    return sorted(rows, key=lambda r: r[1])
+
+
+def tail_breakdown(rows: list[tuple[str, int, int]], steps: int, *, tail_ms: float | None = None,
+                   marker: str | None = None) -> dict[str, Any]:
+    """Kernel time per step over the last ``steps`` steps of a trace (e.g. the
+    replayed decode steps that end a run). The window is either the last
+    ``tail_ms`` of the trace, or -- exact -- from the end of the ``steps + 1``-th
+    last launch of a kernel whose name contains ``marker`` (one launch per
+    step, such as the argmax) to the end of the last one."""
+    if marker is not None:
+        marks = [r for r in rows if marker in r[0]]
+        if len(marks) < steps + 1:
+            raise ValueError(f"{len(marks)} launches of {marker!r}, need {steps + 1}")
+        begin, end = marks[-(steps + 1)][2], marks[-1][2]
+        window = [r for r in rows if r[1] >= begin and r[2] <= end]
+    elif tail_ms is not None:
+        end = rows[-1][2]
+        window = [r for r in rows if r[1] >= end - tail_ms * 1e6]
+    else:
+        raise ValueError("give tail_ms or marker")
+    per: dict[str, list[int]] = {}
+    for name, t0, t1 in window:
+        per.setdefault(name, []).append(t1 - t0)
+    span_ns = end - (begin if marker is not None else window[0][1])
+    kernels = sorted(({"name": n, "calls_per_step": len(d) / steps, "us_per_step": sum(d) / steps / 1e3}
+                      for n, d in per.items()), key=lambda k: -k["us_per_step"])
+    return {"steps": steps, "span_us_per_step": span_ns / steps / 1e3,
+            "busy_us_per_step": sum(k["us_per_step"] for k in kernels), "kernels": kernels}
+
+
+def breakdown_markdown(result: dict[str, Any], command: str, title: str, top: int = 25) -> str:
+    lines = [f"# {title}", "", "Command:", "", "```", command, "```", "",
+             f"Last {result['steps']} steps of the trace: {result['span_us_per_step']:.1f} us per step, "
+             f"{result['busy_us_per_step']:.1f} us of it in kernels.", "",
+             "| kernel | calls / step | us / step | share |", "|---|---:|---:|---:|"]
+    for k in result["kernels"][:top]:
+        name = k["name"] if len(k["name"]) <= 110 else k["name"][:107] + "..."
+        share = 100.0 * k["us_per_step"] / result["span_us_per_step"]
+        lines.append(f"| `{name}` | {k['calls_per_step']:.1f} | {k['us_per_step']:.1f} | {share:.1f}% |")
+    return "\n".join(lines) + "\n"
+
+
 def load_traffic_md(path: Path) -> dict[str, int]:
     """``cell -> hbm_bytes_per_launch`` from the machine-readable lines of a summary."""
     out = {}
@@ -153,15 +201,24 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--write", type=Path)
     ap.add_argument("--manifest", type=Path)
     ap.add_argument("--stats", type=Path, help="a *_kernel_stats.csv to summarise instead")
+    ap.add_argument("--trace", type=Path, help="a *_kernel_trace.csv: per-step breakdown of its tail")
+    ap.add_argument("--tail-ms", type=float, default=None, help="with --trace: window at the end of the run")
+    ap.add_argument("--steps", type=int, default=None, help="with --trace: steps inside the window")
+    ap.add_argument("--marker", default=None, help="with --trace: a kernel launched once per step")
     ap.add_argument("--title", default="rocprofv3 kernel statistics")
     ap.add_argument("--command", default="")
     ap.add_argument("--md", type=Path, required=True)
     ap.add_argument("--json", type=Path, help="also write the figures as JSON (e.g. next to a BenchmarkReport)")
     args = ap.parse_args(argv)
-    if args.stats:
+    if args.trace:
+        result = tail_breakdown(read_kernel_trace(args.trace), args.steps, tail_ms=args.tail_ms,
+                                marker=args.marker)
+        args.md.write_text(breakdown_markdown(result, args.command, args.title))
+        record: dict[str, Any] = {"kind": "trace_tail_breakdown", "title": args.title, **result}
+    elif args.stats:
         rows = read_kernel_stats(args.stats)
         args.md.write_text(stats_markdown(rows, args.command, args.title))
-        record: dict[str, Any] = {"kind": "kernel_stats", "title": args.title, "kernels": rows}
+        record = {"kind": "kernel_stats", "title": args.title, "kernels": rows}
     else:
         result = traffic(args.fetch, args.write, args.manifest)
         args.md.write_text(to_markdown(result, args.command))

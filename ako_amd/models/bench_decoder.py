@@ -11,7 +11,7 @@ generated tokens so the two backends can be compared. Prefill is the median of
 run with every decode step replayed from a HIP graph (``GraphedGreedy``),
 which removes the per-launch host cost that dominates batch-1 decoding.
 
-    python -m ako_amd.models.bench_decoder [--steps 128] [--prompt 512]
+    python -m ako_amd.models.bench_decoder [--steps 128] [--prompt 512] [--backend ako]
 """
 
 from __future__ import annotations
@@ -125,11 +125,18 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--repeats", type=int, default=3)
+    ap.add_argument("--backend", choices=("torch", "ako"), default=None,
+                    help="run one backend only (e.g. under a profiler) instead of comparing both")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("configs[4] needs a GPU", file=sys.stderr)
         return 1
-    print(json.dumps(compare(args.prompt, args.steps, args.repeats)), flush=True)
+    if args.backend:
+        out = run_config5(args.backend, prompt_len=args.prompt, decode_steps=args.steps, repeats=args.repeats)
+        out.pop("tokens")
+    else:
+        out = compare(args.prompt, args.steps, args.repeats)
+    print(json.dumps(out), flush=True)
     return 0
 
 

@@ -1,0 +1,95 @@
+"""rocprofv3 output parsing on synthetic files (no GPU, no profiler).
+
+The counter arithmetic is what ``bench.py``'s ``roofline.traffic`` rests on:
+per-dispatch ``FETCH_SIZE`` / ``WRITE_SIZE`` (KiB, summed over the counter's
+instances) are matched to the launch manifest from the end of the run, then
+scaled by the reading of the plain elementwise reference of known traffic.
+"""
+
+from __future__ import annotations
+
+import csv
+import json
+from pathlib import Path
+
+import pytest
+
+from ako_amd.benchmark import rocprof
+
+COUNTER_FIELDS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+
+
+def _counter_csv(path: Path, counter: str, values_kib: list[list[float]]) -> Path:
+    """One row per counter instance; dispatch i has the instance values values_kib[i]."""
+    with open(path, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=COUNTER_FIELDS)
+        w.writeheader()
+        w.writerow({"Dispatch_Id": 0, "Kernel_Name": "setup", "Counter_Name": counter, "Counter_Value": 7})
+        for i, parts in enumerate(values_kib, start=1):
+            for v in parts:
+                w.writerow({"Dispatch_Id": i, "Kernel_Name": f"k{i}", "Counter_Name": counter, "Counter_Value": v})
+                w.writerow({"Dispatch_Id": i, "Kernel_Name": f"k{i}", "Counter_Name": "OTHER", "Counter_Value": 1e9})
+    return path
+
+
+def test_traffic_is_scaled_by_the_reference_kernel(tmp_path) -> None:
+    gib = 1 << 30
+    manifest = {"dispatches": [
+        {"cell": "cell_a", "alg_bytes": 3 * (1 << 20)},
+        {"cell": "cell_a", "alg_bytes": 3 * (1 << 20)},
+        {"cell": "reference_neg_fp16_1GiB", "alg_bytes": 2 * gib},
+    ]}
+    (tmp_path / "m.json").write_text(json.dumps(manifest))
+    # FETCH reads half scale (as on MI355X), WRITE full scale; two instances per dispatch.
+    fetch = _counter_csv(tmp_path / "f.csv", "FETCH_SIZE", [[512, 512], [512, 512], [gib / 2048 / 2] * 2])
+    write = _counter_csv(tmp_path / "w.csv", "WRITE_SIZE", [[512, 512], [512, 512], [gib / 1024 / 2] * 2])
+    out = rocprof.traffic(fetch, write, tmp_path / "m.json")
+    assert out["fetch_factor"] == pytest.approx(2.0) and out["write_factor"] == pytest.approx(1.0)
+    cell = out["kernels"]["cell_a"]
+    assert cell["fetch_bytes"] == 2 * (1 << 20) and cell["write_bytes"] == 1 << 20
+    assert cell["traffic_over_alg"] == pytest.approx(1.0)
+    # The markdown's machine-readable lines are what bench.py reads back.
+    md = tmp_path / "t.md"
+    md.write_text(rocprof.to_markdown(out, "cmd"))
+    assert rocprof.load_traffic_md(md) == {"cell_a": cell["hbm_bytes_per_launch"]}
+
+
+def test_traffic_rejects_a_short_run(tmp_path) -> None:
+    manifest = {"dispatches": [{"cell": "c", "alg_bytes": 1}] * 3}
+    (tmp_path / "m.json").write_text(json.dumps(manifest))
+    f = _counter_csv(tmp_path / "f.csv", "FETCH_SIZE", [[1.0]])
+    with pytest.raises(ValueError, match="manifest"):
+        rocprof.traffic(f, f, tmp_path / "m.json")
+
+
+def test_kernel_stats_and_trace_tail(tmp_path) -> None:
+    stats = tmp_path / "s.csv"
+    stats.write_text('"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"\n'
+                     '"kern",4,400,100.0,80.0,90,110,5.0\n')
+    rows = rocprof.read_kernel_stats(stats)
+    assert rows[0]["calls"] == 4 and rows[0]["avg_ns"] == 100.0
+    assert "| `kern` | 4 | 0.10 |" in rocprof.stats_markdown(rows, "cmd", "t")
+
+    trace = tmp_path / "t.csv"
+    with open(trace, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        w.writerow({"Kernel_Name": "warmup", "Start_Timestamp": 0, "End_Timestamp": 5_000_000})
+        t = 10_000_000
+        for _ in range(4):  # four steps of 1 ms: gemv 600 us, norm 100 us
+            w.writerow({"Kernel_Name": "gemv", "Start_Timestamp": t, "End_Timestamp": t + 600_000})
+            w.writerow({"Kernel_Name": "norm", "Start_Timestamp": t + 700_000, "End_Timestamp": t + 800_000})
+            t += 1_000_000
+    rows = rocprof.read_kernel_trace(trace)
+    out = rocprof.tail_breakdown(rows, 4, tail_ms=3.9)
+    by = {k["name"]: k for k in out["kernels"]}
+    assert "warmup" not in by
+    assert by["gemv"]["us_per_step"] == pytest.approx(600.0) and by["norm"]["calls_per_step"] == 1.0
+    assert out["busy_us_per_step"] == pytest.approx(700.0)
+    assert "| `gemv` | 1.0 | 600.0 |" in rocprof.breakdown_markdown(out, "cmd", "t")
+    # Marker windows: norm ends each step; the last 3 steps lie between its 4th-last and last launch.
+    marked = rocprof.tail_breakdown(rows, 3, marker="norm")
+    assert marked["span_us_per_step"] == pytest.approx(1000.0)
+    assert {k["name"]: k["calls_per_step"] for k in marked["kernels"]} == {"gemv": 1.0, "norm": 1.0}
+    with pytest.raises(ValueError, match="need"):
+        rocprof.tail_breakdown(rows, 9, marker="norm")
