@@ -17,8 +17,9 @@ Also reported on the same line:
   decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
                 128 greedy steps, eager PyTorch vs the dispatcher, each also
                 with decode steps replayed from a HIP graph;
-  cpu_baseline  the reference's unfused PyTorch path (ako_amd.ops.*_ref) on
-                host CPU tensors, same grid, a bounded row sample.
+  cpu_baseline  the oracle (numpy port of the reference's unfused path, one
+                thread) on the same grid with a bounded row sample, and beside
+                it the restated PyTorch reference on host CPU tensors.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
 """
@@ -225,45 +226,75 @@ def main() -> int:
             f"(graphed {decoder['ako'].get('graphed_decode_ms_per_step')} ms)")
         torch.cuda.empty_cache()
 
-    # ---- CPU baseline: the reference's unfused PyTorch path on host cores ------
+    # ---- CPU baseline: the oracle (a CPU port of the reference's algorithm) ------
+    # The oracle (numpy, single-threaded) is the primary figure, as a "port" of
+    # the reference's unfused path; the restated PyTorch reference on host
+    # tensors (multi-threaded) is reported beside it. Both run the 12 cells of
+    # the step on a bounded row sample, timed by wall clock for ~cpu-seconds.
     cpu = None
     if not args.no_cpu:
+        import numpy as np
+
         from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
+        from oracle import ops as oracle
+
+        def storage(t: "torch.Tensor") -> "np.ndarray":
+            if t.dtype == torch.bfloat16:
+                return t.view(torch.int16).numpy().view(np.uint16)
+            return t.numpy()
+
+        def timed_passes(cells: list, seconds: float) -> tuple[int, float]:
+            for _, fn in cells:
+                fn()
+            passes, t0 = 0, time.perf_counter()
+            while True:
+                for _, fn in cells:
+                    fn()
+                passes += 1
+                elapsed = time.perf_counter() - t0
+                if elapsed >= seconds and passes >= 3:
+                    return passes, elapsed
 
         sample_rows = 64
         g = torch.Generator().manual_seed(0)
-        host = []
+        port_cells, torch_cells = [], []
         for dtype in (torch.float16, torch.bfloat16):
+            name = "float16" if dtype == torch.float16 else "bfloat16"
             for h in RMS_HIDDEN:
                 x = torch.randn(sample_rows, h, generator=g).to(dtype)
                 r = torch.randn(sample_rows, h, generator=g).to(dtype)
                 w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
-                host.append((rf.alg_bytes_rmsnorm(sample_rows, h, dtype), lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
-                host.append((rf.alg_bytes_rmsnorm_residual(sample_rows, h, dtype),
-                             lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
-        for _, fn in host:
-            fn()
-        passes, t0 = 0, time.perf_counter()
-        while True:
-            for _, fn in host:
-                fn()
-            passes += 1
-            elapsed = time.perf_counter() - t0
-            if elapsed >= args.cpu_seconds and passes >= 3:
-                break
-        cpu_gbps = sum(b for b, _ in host) * passes / elapsed / 1e9
+                xn, rn, wn = storage(x), storage(r), storage(w)
+                b_plain = rf.alg_bytes_rmsnorm(sample_rows, h, dtype)
+                b_res = rf.alg_bytes_rmsnorm_residual(sample_rows, h, dtype)
+                port_cells.append((b_plain, lambda xn=xn, wn=wn, name=name: oracle.rmsnorm(xn, wn, 1e-6, dtype=name)))
+                port_cells.append((b_res, lambda xn=xn, rn=rn, wn=wn, name=name:
+                                   oracle.rmsnorm_residual(xn, rn, wn, 1e-6, dtype=name)))
+                torch_cells.append((b_plain, lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
+                torch_cells.append((b_res, lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
+        passes, elapsed = timed_passes(port_cells, args.cpu_seconds)
+        port_gbps = sum(b for b, _ in port_cells) * passes / elapsed / 1e9
+        t_passes, t_elapsed = timed_passes(torch_cells, args.cpu_seconds / 2)
+        torch_gbps = sum(b for b, _ in torch_cells) * t_passes / t_elapsed / 1e9
         cpu = {
-            "value": round(cpu_gbps, 3),
+            "value": round(port_gbps, 3),
             "unit": "GB/s",
-            "cores": torch.get_num_threads(),
+            "cores": 1,
             "kind": "port",
-            "sample": (f"ako_amd.ops.rmsnorm_ref / rmsnorm_residual_ref (the reference's unfused "
-                       f"PyTorch path) on CPU tensors: the same 12 cells with {sample_rows} rows "
-                       f"instead of {RMS_ROWS}, {passes} passes in {elapsed:.1f} s; "
-                       f"os.cpu_count()={os.cpu_count()}"),
-            "gpu_speedup": round(value / cpu_gbps, 1) if cpu_gbps > 0 else None,
+            "sample": (f"oracle.ops.rmsnorm / rmsnorm_residual (numpy restatement of the reference's "
+                       f"unfused path, one thread) on the same 12 cells with {sample_rows} rows instead "
+                       f"of {RMS_ROWS}: {passes} passes in {elapsed:.1f} s"),
+            "gpu_speedup": round(value / port_gbps, 1) if port_gbps > 0 else None,
+            "torch_cpu": {
+                "value": round(torch_gbps, 3),
+                "cores": torch.get_num_threads(),
+                "sample": (f"ako_amd.ops.rmsnorm_ref / rmsnorm_residual_ref (the reference's PyTorch "
+                           f"path) on host tensors, same cells: {t_passes} passes in {t_elapsed:.1f} s; "
+                           f"os.cpu_count()={os.cpu_count()}"),
+            },
         }
-        log(f"cpu baseline: {cpu_gbps:.3f} GB/s on {torch.get_num_threads()} threads")
+        log(f"cpu baseline: oracle {port_gbps:.3f} GB/s on 1 thread, torch CPU {torch_gbps:.3f} GB/s "
+            f"on {torch.get_num_threads()} threads")
 
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op/shape; 4-layer decoder prefill+decode ms",
