@@ -1,0 +1,171 @@
+"""Error bounds of the product's PyTorch references, derived in fp64, and the
+selector property that a chosen kernel always passes the gate.
+
+Follows the test strategy of the reference's ``tests/test_numerical_bounds.py``
+(derived bounds for RMSNorm, RoPE and SwiGLU; candidates against native
+error; a property test of selection), written against this package. Inputs
+are seeded and hypothesis runs derandomized, so the suite is deterministic.
+
+Bounds: ``u`` is the unit roundoff of the storage dtype (2^-11 fp16, 2^-8
+bf16, 2^-24 fp32), ``u32`` that of the fp32 compute type, ``eta`` half the
+smallest subnormal of the storage dtype (an absolute floor for results that
+underflow). A result computed in fp32 with relative error ``d32`` and then
+rounded to storage satisfies ``|y - y64| <= (u + (1 + u) d32) |y64| + eta``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from ako_amd.dispatcher.cache import KernelCache
+from ako_amd.dispatcher.registry import KernelEntry, KernelRegistry
+from ako_amd.dispatcher.selector import KernelSelector
+from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
+from ako_amd.ops.rmsnorm_torch import rmsnorm_torch_native
+from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
+from ako_amd.ops.swiglu_ref import swiglu_ref
+from ako_amd.validation.numerical import error_budget, max_abs_error
+
+U = {torch.float16: 2.0**-11, torch.bfloat16: 2.0**-8, torch.float32: 2.0**-24}
+ETA = {torch.float16: 2.0**-25, torch.bfloat16: 2.0**-134, torch.float32: 2.0**-150}
+U32 = 2.0**-24
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+SETTINGS = settings(max_examples=25, derandomize=True, deadline=None)
+
+
+def _randn(shape, seed, scale=1.0, shift=0.0) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float64) * scale + shift
+
+
+def _within(y: torch.Tensor, y64: torch.Tensor, dtype: torch.dtype, d32: float) -> torch.Tensor:
+    u = U[dtype]
+    bound = (u + (1 + u) * d32) * y64.abs() + ETA[dtype]
+    return (y.double() - y64).abs() <= bound
+
+
+@SETTINGS
+@given(n=st.sampled_from([3, 17, 100, 257, 1000, 2049, 4095, 8191]),
+       dtype=st.sampled_from(DTYPES), seed=st.integers(0, 2**16))
+def test_rmsnorm_ref_within_derived_bound(n: int, dtype: torch.dtype, seed: int) -> None:
+    """fp32 sum of n squares (recursive-summation worst case, gamma_n), one
+    division by n, sqrt and reciprocal, two products: d32 <= (n + 6) u32."""
+    x = (_randn((4, n), seed, scale=3.0)).to(dtype)
+    w = (_randn((n,), seed + 1, scale=0.1, shift=1.0)).to(dtype)
+    y = rmsnorm_ref(x, w, 1e-6)
+    x64, w64 = x.double(), w.double()
+    y64 = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6) * w64
+    assert _within(y, y64, dtype, (n + 6) * U32).all()
+
+
+def test_rmsnorm_bound_catches_a_dropped_weight() -> None:
+    """The bound is tight enough that omitting the weight (w ~ N(1, 0.1)) fails it."""
+    x = _randn((4, 1000), 3).to(torch.float16)
+    w = _randn((1000,), 4, scale=0.1, shift=1.0).to(torch.float16)
+    x64 = x.double()
+    y64 = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+    wrong = rmsnorm_ref(x, torch.ones_like(w), 1e-6)
+    assert not _within(wrong, y64, torch.float16, 1006 * U32).all()
+
+
+def test_rope_is_orthogonal_in_fp64() -> None:
+    """With fp64 tables and input the rotation preserves every pair's norm."""
+    x = _randn((2, 64, 4, 32), 5)
+    cos, sin = build_rope_tables(64, 32, device="cpu", dtype=torch.float64)
+    for style in ("neox", "interleaved"):
+        y = rope_ref(x, cos, sin, style)
+        if style == "neox":
+            a, b, ya, yb = x[..., :16], x[..., 16:], y[..., :16], y[..., 16:]
+        else:
+            a, b, ya, yb = x[..., 0::2], x[..., 1::2], y[..., 0::2], y[..., 1::2]
+        torch.testing.assert_close(torch.hypot(ya, yb), torch.hypot(a, b), rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("offset", [0, 1000, 100_000])
+def test_rope_table_error_bounded_and_grows_with_position(offset: int) -> None:
+    """fp32 tables form theta = pos * inv_freq in fp32: |d theta| <= 2 u32 |theta|
+    (inv_freq and the product each round once), so |d cos|, |d sin| <=
+    2 u32 |theta| + u32, a bound that grows with the position."""
+    seq, d = 256, 128
+    c32, s32 = build_rope_tables(seq, d, offset=offset, device="cpu", dtype=torch.float32)
+    half = d // 2
+    inv = 1.0 / (10000.0 ** (torch.arange(half, dtype=torch.float64) * 2.0 / d))
+    theta = torch.outer(torch.arange(offset, offset + seq, dtype=torch.float64), inv)
+    err = torch.maximum((c32.double() - theta.cos()).abs(), (s32.double() - theta.sin()).abs())
+    bound = 2 * U32 * theta.abs() + U32
+    assert (err <= bound * 1.0001).all()
+    if offset >= 1000:  # far from the origin the error is dominated by the angle term
+        assert err.max().item() > 4 * U32
+
+
+@SETTINGS
+@given(n=st.sampled_from([1, 7, 100, 1001, 8448]), dtype=st.sampled_from(DTYPES),
+       seed=st.integers(0, 2**16))
+def test_swiglu_first_order_propagation(n: int, dtype: torch.dtype, seed: int) -> None:
+    """silu(g) * u in fp32: exp, one add, one division, one product;
+    d32 <= 8 u32 relative to the fp64 result (exp error included)."""
+    g = _randn((3, n), seed, scale=4.0).to(dtype)
+    u = _randn((3, n), seed + 1).to(dtype)
+    y = swiglu_ref(g, u)
+    g64, u64 = g.double(), u.double()
+    y64 = g64 / (1 + torch.exp(-g64)) * u64
+    assert _within(y, y64, dtype, 8 * U32).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_reference_within_twice_native_error(dtype: torch.dtype) -> None:
+    """The unfused reference is no worse than twice the native kernel's error
+    (``F.rms_norm``) against fp64, plus one storage ulp of slack."""
+    x = _randn((64, 4096), 6, scale=2.0).to(dtype)
+    w = _randn((4096,), 7, scale=0.1, shift=1.0).to(dtype)
+    x64 = x.double()
+    y64 = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+    ref_err = (rmsnorm_ref(x, w, 1e-6).double() - y64).abs().max().item()
+    nat_err = (rmsnorm_torch_native(x, w, 1e-6).double() - y64).abs().max().item()
+    slack = U[dtype] * y64.abs().max().item()
+    assert ref_err <= 2 * nat_err + slack
+    assert nat_err <= 2 * ref_err + slack
+
+
+def _offset_kernel(k: float, budget: float):
+    def fn(x, weight, eps=1e-6):
+        return rmsnorm_ref(x, weight, eps) + k * budget
+    return fn
+
+
+@settings(max_examples=15, derandomize=True, deadline=None)
+@given(ks=st.lists(st.sampled_from([0.0, 0.25, 0.5, 0.9, 1.25, 2.0, 4.0]), min_size=1, max_size=4))
+def test_selected_kernel_always_passes_the_gate(tmp_path_factory, ks: list[float]) -> None:
+    """Candidates off the reference by k budgets, the worst ones fastest: the
+    selector may pick any candidate with k < 1 (or the reference), never one
+    outside the budget, whatever the timings."""
+    x = _randn((8, 256), 11).float()
+    w = torch.ones(256)
+    budget = error_budget(rmsnorm_ref(x, w, 1e-6))
+
+    def slow_ref(x, weight, eps=1e-6):
+        return rmsnorm_ref(x, weight, eps) + 0.0 * math.fsum([1.0] * 2000)
+
+    reg = KernelRegistry()
+    reg.register(KernelEntry("rmsnorm", "rmsnorm_ref", slow_ref, backend="pytorch", priority=10))
+    for i, k in enumerate(ks):
+        reg.register(KernelEntry("rmsnorm", f"cand{i}_k{k}", _offset_kernel(k, budget), backend="fake",
+                                 priority=5))
+    cache = KernelCache(path=tmp_path_factory.mktemp("sel") / "cache.json")
+    selector = KernelSelector(registry=reg, cache=cache, warmup=1, repeats=3, allow_cpu_tuning=True)
+    result = selector.select_entry("rmsnorm", x, w)
+    assert result.source == "benchmark"
+    chosen = result.entry.kernel_name
+    if chosen != "rmsnorm_ref":
+        k = float(chosen.split("_k")[1])
+        assert k < 1.0, (chosen, ks)
+    out = result.entry.fn(x, w, 1e-6)
+    assert max_abs_error(rmsnorm_ref(x, w, 1e-6), out) <= budget
+    rejected = {r.split(":")[0] for r in result.rejected}
+    assert {f"cand{i}_k{k}" for i, k in enumerate(ks) if k > 1.0} <= rejected
