@@ -94,6 +94,30 @@ class KVCache:
     def length(self) -> int:
         return self.lengths[0]
 
+    def slab_tail(self, layer_idx: int, k: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, int]:
+        """The next ``k.shape[1]`` free slots of the preallocated slabs, viewed
+        heads-major ``(batch, kv_heads, seq, head_dim)`` (the layout
+        ``rope_qk_cache`` addresses), and the first of them. Only for a cache
+        with ``max_len``."""
+        start, add = self.lengths[layer_idx], k.shape[1]
+        if start + add > self.max_len:
+            raise ValueError(f"KV cache overflow: {start + add} > max_len {self.max_len}")
+        slab = self.entries[layer_idx]
+        if slab is None:
+            shape = (k.shape[0], self.max_len, k.shape[2], k.shape[3])
+            slab = (k.new_empty(shape), k.new_empty(shape))
+            self.entries[layer_idx] = slab
+        end = start + add
+        return slab[0][:, start:end].transpose(1, 2), slab[1][:, start:end].transpose(1, 2), start
+
+    def advance(self, layer_idx: int, added: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Count ``added`` tokens written through :meth:`slab_tail`; returns the
+        filled part of this layer's cache, ``(batch, seq, heads, dim)``."""
+        end = self.lengths[layer_idx] + added
+        self.lengths[layer_idx] = end
+        slab = self.entries[layer_idx]
+        return slab[0][:, :end], slab[1][:, :end]
+
     def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Append ``(k, v)`` and return views of the whole cache of this layer."""
         start, add = self.lengths[layer_idx], k.shape[1]
@@ -196,6 +220,17 @@ def _rope(backend: Backend, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tenso
     return rope(x, cos, sin, style, kernel=(override or {}).get("rope"))
 
 
+_ZERO_POSITIONS: dict[torch.device, torch.Tensor] = {}
+
+
+def _zero_position(device: torch.device) -> torch.Tensor:
+    """A one-element int64 zero on ``device``, made once per device."""
+    t = _ZERO_POSITIONS.get(device)
+    if t is None:
+        t = _ZERO_POSITIONS[device] = torch.zeros(1, dtype=torch.long, device=device)
+    return t
+
+
 def _fused_cache_rope(backend: Backend, override: KernelOverride | None) -> bool:
     """Whether a static-cache decode step rotates q/k and appends k/v to the
     cache in one call (``rope_qk_cache``) instead of RoPE plus two copies.
@@ -238,6 +273,16 @@ class Attention(nn.Module):
                 vh = vh.repeat_interleave(self.repeats, dim=1)
             attn = F.scaled_dot_product_attention(q.transpose(1, 2), kh, vh, attn_mask=kv_cache.mask)
             return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
+        if (isinstance(kv_cache, KVCache) and kv_cache.max_len is not None
+                and _fused_cache_rope(self.backend, self.kernel_override)):
+            # Preallocated host-tracked cache: rotate q and write rotated k and v
+            # into the slab from the first free slot on, in one call. cos/sin are
+            # the rows of positions [start, start + seq), so position 0 of the
+            # call is the free slot itself.
+            kc, vc, _ = kv_cache.slab_tail(layer_idx, k)
+            q = rope_qk_cache(q, k, v, cos, sin, _zero_position(q.device), kc, vc, cfg.rope_style)
+            k, v = kv_cache.advance(layer_idx, seq_len)
+            return self._attend(q, k, v, batch, seq_len)
         if self.backend == "ako" and not (self.kernel_override or {}).get("rope"):
             # One dispatched op (a single launch on the HIP path) for both tensors.
             q, k = rope_qk(q, k, cos, sin, cfg.rope_style,
@@ -255,13 +300,17 @@ class Attention(nn.Module):
             return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
         if kv_cache is not None:
             k, v = kv_cache.update(layer_idx, k, v)
+        return self._attend(q, k, v, batch, seq_len)
+
+    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
+        """SDPA over ``(batch, seq, heads, dim)`` q and cached k/v, then the output projection."""
         if self.repeats > 1:
             k = k.repeat_interleave(self.repeats, dim=2)
             v = v.repeat_interleave(self.repeats, dim=2)
         attn = F.scaled_dot_product_attention(
             q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=seq_len > 1
         )
-        return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, cfg.hidden_dim))
+        return self.o_proj(attn.transpose(1, 2).reshape(batch, seq_len, self.config.hidden_dim))
 
 
 class MLP(nn.Module):
