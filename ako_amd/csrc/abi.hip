@@ -112,6 +112,7 @@ int ako_set_tuning(int op, int key, int value) {
         return AKO_OK;
       }
       if (key == 6) { ako::g_rms_tuning.xcd_chunk = value; return AKO_OK; }
+      if (key == 7) { ako::g_rms_tuning.max_blocks = value; return AKO_OK; }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

@@ -75,8 +75,8 @@ __device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, unsigned
 template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
-    T* __restrict__ y, T* __restrict__ rout, int64_t rows, int hidden, int64_t sx, int64_t sr,
-    int64_t sy, int64_t srout, float inv_h, float eps, unsigned xcd_chunk) {
+    T* __restrict__ y, T* __restrict__ rout, int64_t row0, int64_t rows, int hidden, int64_t sx,
+    int64_t sr, int64_t sy, int64_t srout, float inv_h, float eps, unsigned xcd_chunk) {
   constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per packet
   constexpr int TPR = kWave * WPR;                     // lanes per row
   // Packets are processed in groups: every load of a group is issued before
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   const int row_in_block = wave / WPR;
   const int wave_in_row = wave - row_in_block * WPR;
   const int t = wave_in_row * kWave + lane;
-  const int64_t row = static_cast<int64_t>(block_order(blockIdx.x, gridDim.x, xcd_chunk)) * RPB + row_in_block;
+  const int64_t row = row0 + static_cast<int64_t>(block_order(blockIdx.x, gridDim.x, xcd_chunk)) * RPB + row_in_block;
   const bool active = row < rows;
   const int nvec = hidden / E;
   const int tail = hidden - nvec * E;
@@ -196,10 +196,10 @@ constexpr int kStreamBlock = 256;
 template <typename T, typename W, int E, bool RES>
 __global__ __launch_bounds__(kStreamBlock) void rmsnorm_stream(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
-    T* __restrict__ y, T* __restrict__ rout, int hidden, int64_t sx, int64_t sr, int64_t sy,
-    int64_t srout, float inv_h, float eps) {
+    T* __restrict__ y, T* __restrict__ rout, int64_t row0, int hidden, int64_t sx, int64_t sr,
+    int64_t sy, int64_t srout, float inv_h, float eps) {
   using P = Pack<T, E>;
-  const int64_t row = blockIdx.x;
+  const int64_t row = row0 + blockIdx.x;
   const int tid = threadIdx.x;
   const int nvec = hidden / E;
   const int tail = hidden - nvec * E;
@@ -316,11 +316,22 @@ RegShape pick_shape(int64_t nvec, bool residual) {
 
 constexpr unsigned kXcdChunk = 8;
 
+// Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
+// the dispatch packet never wraps; larger problems take several launches,
+// each starting at row0. ako_set_tuning(0, 7, n) lowers the cap (tests
+// exercise the split at small sizes with it).
+int64_t max_blocks_per_launch(int threads_per_block) {
+  const int64_t cap = (int64_t(1) << 31) / threads_per_block;
+  const int64_t forced = g_rms_tuning.max_blocks;
+  return forced > 0 ? std::min(cap, forced) : cap;
+}
+
 template <typename T, typename W, int WPR, int VPT, bool RES>
 hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
-  const dim3 grid(static_cast<unsigned>(ceil_div(a.rows, RPB)));
   const dim3 block(kWave * WPR * RPB);
+  const int64_t total_blocks = ceil_div(a.rows, RPB);
+  const int64_t cap = max_blocks_per_launch(kWave * WPR * RPB);
   // A residual row of >= 32 KiB per tensor keeps 4 x 32 KiB in flight; two
   // such rows per CU exceed the CU's share of its XCD's L2 (4 MiB / 32 CUs),
   // so an LDS reservation above half the CU's 160 KiB limits those launches to
@@ -335,16 +346,21 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   // rows, -1-2% at 8 KiB rows; whole-grid runs (chunk = n / 8) lose up to 12%
   // at 8 KiB rows.
   const bool wide = a.hidden * static_cast<int64_t>(sizeof(T)) >= 16 * 1024;
-  unsigned xcd_chunk = wide && grid.x >= 8 * kXcdChunk ? kXcdChunk : 1;
-  if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
-  if (g_rms_tuning.row_order == 2)
-    xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
-  hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid, block, lds,
-                     stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
-                     static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
-                     a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
-                     1.0f / static_cast<float>(a.hidden), a.eps, xcd_chunk);
-  return hipGetLastError();
+  for (int64_t b0 = 0; b0 < total_blocks; b0 += cap) {
+    const dim3 grid(static_cast<unsigned>(std::min(cap, total_blocks - b0)));
+    unsigned xcd_chunk = wide && grid.x >= 8 * kXcdChunk ? kXcdChunk : 1;
+    if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
+    if (g_rms_tuning.row_order == 2)
+      xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
+    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid,
+                       block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                       static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
+                       b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
+                       1.0f / static_cast<float>(a.hidden), a.eps, xcd_chunk);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 template <typename T, typename W, bool RES>
@@ -377,7 +393,6 @@ hipError_t run_reg_shape(const RegShape& s, const RmsArgs& a, hipStream_t stream
 
 template <typename T, typename W, bool RES>
 hipError_t run_stream(const RmsArgs& a, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(a.rows));
   const float inv_h = 1.0f / static_cast<float>(a.hidden);
   const auto* x = static_cast<const T*>(a.x);
   const auto* r = static_cast<const T*>(a.r);
@@ -385,14 +400,20 @@ hipError_t run_stream(const RmsArgs& a, hipStream_t stream) {
   auto* y = static_cast<T*>(a.y);
   auto* ro = static_cast<T*>(a.rout);
   const int h = static_cast<int>(a.hidden);
-  if (a.vector_ok) {
-    hipLaunchKernelGGL((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
-                       stream, x, r, w, y, ro, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
-  } else {
-    hipLaunchKernelGGL((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
-                       w, y, ro, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+  const int64_t cap = max_blocks_per_launch(kStreamBlock);
+  for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
+    const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
+    if (a.vector_ok) {
+      hipLaunchKernelGGL((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
+                         stream, x, r, w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+    } else {
+      hipLaunchKernelGGL((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
+                         w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
   }
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 template <typename T, typename W>

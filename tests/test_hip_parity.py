@@ -194,6 +194,32 @@ def test_rmsnorm_xcd_row_orders_cover_every_row(rows: int) -> None:
             _native.set_tuning(0, key, 0)
 
 
+@pytest.mark.parametrize("cap", [1, 3, 7, 64])
+def test_rmsnorm_split_launches_match_one_launch(cap: int) -> None:
+    """Problems past the per-launch workgroup cap run as several launches from
+    row offsets; with the cap lowered (key 7) the split path must reproduce the
+    single launch bit for bit, for packed-row, wide-row and two-pass kernels."""
+    from ako_amd import _native
+
+    cases = [(301, 256), (259, 4096), (97, 140_000)]  # 4 rows per block, XCD-ordered wide rows, two-pass
+    try:
+        for rows, hidden in cases:
+            x = grandn((rows, hidden), torch.bfloat16, 33)
+            r = grandn((rows, hidden), torch.bfloat16, 34)
+            w = grandn((hidden,), torch.bfloat16, 35, scale=0.1, shift=1.0)
+            _native.set_tuning(0, 7, 0)
+            want_p = rmsnorm_hip(x, w)
+            want_y, want_s = rmsnorm_residual_hip(x, r, w)
+            _native.set_tuning(0, 7, cap)
+            assert torch.equal(rmsnorm_hip(x, w), want_p), (rows, hidden, cap)
+            y, s = rmsnorm_residual_hip(x, r, w)
+            assert torch.equal(y, want_y) and torch.equal(s, want_s), (rows, hidden, cap)
+        ey = oracle.rmsnorm(to_np(x), to_np(w), dtype="bfloat16")
+        assert_oracle(ey, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
+    finally:
+        _native.set_tuning(0, 7, 0)
+
+
 def test_rmsnorm_empty_and_errors() -> None:
     w = torch.ones(64, device=DEV, dtype=torch.float16)
     empty = torch.empty(0, 64, device=DEV, dtype=torch.float16)
