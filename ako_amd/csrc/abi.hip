@@ -56,17 +56,33 @@ bool aligned(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }
 
-// Byte range [lo, hi) spanned by `count` rows of `width` elements, `stride` apart.
+// Byte range [lo, hi) spanned by `count` rows of `width` elements, `stride`
+// apart. `ok` is false when the extent exceeds 2^56 bytes or wraps the address
+// space (sizes no allocation can have); the arithmetic is done in 128 bits so
+// that such arguments cannot wrap into a small, plausible-looking span.
+constexpr __int128 kMaxSpanBytes = static_cast<__int128>(1) << 56;
+
 struct Span {
   uintptr_t lo = 0, hi = 0;
+  bool ok = true;
 };
 
-Span span_2d(const void* p, int64_t rows, int64_t width, int64_t stride, int elem) {
+Span span_bytes(const void* p, __int128 bytes) {
   Span s;
   s.lo = reinterpret_cast<uintptr_t>(p);
-  const int64_t last = (rows - 1) * stride + width;
-  s.hi = s.lo + static_cast<uintptr_t>(last) * elem;
+  if (bytes < 0 || bytes > kMaxSpanBytes) {
+    s.ok = false;
+    s.hi = s.lo;
+    return s;
+  }
+  s.hi = s.lo + static_cast<uintptr_t>(bytes);
+  s.ok = s.hi >= s.lo;
   return s;
+}
+
+Span span_2d(const void* p, int64_t rows, int64_t width, int64_t stride, int elem) {
+  const __int128 last = static_cast<__int128>(rows - 1) * stride + width;
+  return span_bytes(p, last * elem);
 }
 
 bool overlap(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
@@ -152,6 +168,9 @@ static int rmsnorm_common(const void* x, const void* r, const void* w, void* y, 
   const Span sy_span = span_2d(y, rows, hidden, sy, eb);
   const Span sx_span = span_2d(x, rows, hidden, sx, eb);
   const Span w_span = span_2d(w, 1, hidden, hidden, ako::dtype_bytes(w_dtype));
+  if (!sy_span.ok || !sx_span.ok ||
+      (residual && (!span_2d(r, rows, hidden, sr, eb).ok || !span_2d(rout, rows, hidden, srout, eb).ok)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
   if (overlap(sy_span, sx_span) || overlap(sy_span, w_span))
     return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output y overlaps an input", fn);
   if (residual) {
@@ -198,10 +217,12 @@ struct RopeTensorIn {
   bool at_pos;        // output rows are cache slots (*pos + s), cache_len of them
 };
 
-// Extent, in elements, of a [n0, n1, n2, head_dim] view with the given
-// strides (last dimension contiguous): offset of the last element + 1.
-int64_t extent4(int64_t n0, int64_t n1, int64_t n2, int64_t d, const int64_t* st) {
-  return (n0 - 1) * st[0] + (n1 - 1) * st[1] + (n2 - 1) * st[2] + d;
+// Byte span of a [n0, n1, n2, head_dim] view with the given element strides
+// (last dimension contiguous): up to the last element + 1.
+Span span_4d(const void* p, int64_t n0, int64_t n1, int64_t n2, int64_t d, const int64_t* st, int elem) {
+  const __int128 last = static_cast<__int128>(n0 - 1) * st[0] + static_cast<__int128>(n1 - 1) * st[1] +
+                        static_cast<__int128>(n2 - 1) * st[2] + d;
+  return span_bytes(p, last * elem);
 }
 
 // True when distinct (i0, i1, i2, e) of a [n0, n1, n2, head_dim] view address
@@ -258,6 +279,8 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
   const int tb = ako::dtype_bytes(table_dtype);
   const Span cos_span = span_2d(cos, tab_rows, head_dim / 2, st, tb);
   const Span sin_span = span_2d(sin, tab_rows, head_dim / 2, st, tb);
+  if (!cos_span.ok || !sin_span.ok)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: table sizes and strides overflow the address space", fn);
   Span out_spans[3], in_spans[3];
   for (int i = 0; i < nt; ++i) {
     const RopeTensorIn& t = ts[i];
@@ -269,10 +292,10 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
     // Distinct output elements must not alias.
     if (!distinct_rows(batch, out_rows, t.heads, head_dim, t.ys))
       return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output strides make rows overlap", fn);
-    in_spans[i] = Span{reinterpret_cast<uintptr_t>(t.x),
-                       reinterpret_cast<uintptr_t>(t.x) + static_cast<uintptr_t>(extent4(batch, seq, t.heads, head_dim, t.xs)) * eb};
-    out_spans[i] = Span{reinterpret_cast<uintptr_t>(t.y),
-                        reinterpret_cast<uintptr_t>(t.y) + static_cast<uintptr_t>(extent4(batch, out_rows, t.heads, head_dim, t.ys)) * eb};
+    in_spans[i] = span_4d(t.x, batch, seq, t.heads, head_dim, t.xs, eb);
+    out_spans[i] = span_4d(t.y, batch, out_rows, t.heads, head_dim, t.ys, eb);
+    if (!in_spans[i].ok || !out_spans[i].ok)
+      return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
   }
   if (cache) {
     const Span pos_span{reinterpret_cast<uintptr_t>(pos), reinterpret_cast<uintptr_t>(pos) + sizeof(int64_t)};
@@ -397,8 +420,11 @@ int ako_swiglu_fwd(const void* gate, const void* up, void* y, int64_t rows, int6
     return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output row stride smaller than n (rows would overlap)", fn);
   const int eb = ako::dtype_bytes(dtype);
   const Span ys = span_2d(y, rows, n, y_row_stride, eb);
-  if (overlap(ys, span_2d(gate, rows, n, gate_row_stride, eb)) ||
-      overlap(ys, span_2d(up, rows, n, up_row_stride, eb)))
+  const Span gs = span_2d(gate, rows, n, gate_row_stride, eb);
+  const Span us = span_2d(up, rows, n, up_row_stride, eb);
+  if (!ys.ok || !gs.ok || !us.ok)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
+  if (overlap(ys, gs) || overlap(ys, us))
     return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output overlaps an input", fn);
   const bool contiguous = rows == 1 || (gate_row_stride == n && up_row_stride == n && y_row_stride == n);
   const bool vec = aligned(gate, 16) && aligned(up, 16) && aligned(y, 16) &&

@@ -152,6 +152,22 @@ def test_swiglu_validation(lib) -> None:
     assert f(None, B, C, 4, 16, 16, 16, 16, BF16, None) == INVALID
 
 
+def test_sizes_that_overflow_the_address_space_are_rejected(lib) -> None:
+    """Extents are computed in 128 bits: huge sizes or strides cannot wrap into
+    a small span that would pass the overlap checks."""
+    big = 2**40
+    assert rms(lib, rows=big, sx=2**30, sy=2**30) == INVALID
+    assert "overflow" in _native.last_error()
+    assert rms(lib, rows=2, sx=2**62, sy=64) == INVALID and "overflow" in _native.last_error()
+    assert lib.ako_swiglu_fwd(A, B, C, 2**50, 2**20, 2**20, 2**20, 2**20, BF16, None) == INVALID
+    assert "overflow" in _native.last_error()
+    huge = (ctypes.c_int64 * 3)(2**61, 16, 8)
+    ok = (ctypes.c_int64 * 3)(64, 16, 8)
+    assert lib.ako_rope_qk_fwd(A, B, C, D, E, 0x600000, 2, 4, 2, 2, 8, huge, ok, ok, ok, 4, F16, F32, 0,
+                               None) == INVALID
+    assert "overflow" in _native.last_error()
+
+
 def test_tuning_keys(lib) -> None:
     assert lib.ako_set_tuning(9, 1, 1) == INVALID
     assert lib.ako_set_tuning(0, 1, -1) == INVALID

@@ -19,7 +19,6 @@ import math
 
 import pytest
 import torch
-import torch.nn.functional as F
 from hypothesis import given, settings
 from hypothesis import strategies as st
 
