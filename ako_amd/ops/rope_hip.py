@@ -20,7 +20,7 @@ import ctypes
 import torch
 
 from ako_amd import _native
-from ako_amd.ops._hip_common import call, dtype_code, gpu_index, lib, raw_stream
+from ako_amd.ops._hip_common import DT, call, dtype_code, gpu_index, lib, raw_stream
 from ako_amd.ops.rope_ref import validate_rope_args
 
 
@@ -107,6 +107,44 @@ def rope_qk_hip(
 
 
 _I64x15 = ctypes.c_int64 * 15
+# Stride arrays by stride tuples: a decoder calls this with the same few layouts
+# every step. The arrays are read-only once built (the library copies the
+# strides during the call), so sharing them between threads is safe.
+_strides_cache: dict[tuple, ctypes.Array] = {}
+
+
+def _cache_args_error(q, k, v, cos, sin, pos, k_cache, v_cache, style) -> str:
+    """The first thing wrong with rope_qk_cache_hip's arguments (slow path)."""
+    if style not in _native.ROPE_STYLE_CODES:
+        return f"Unknown RoPE style {style!r}"
+    if q.dim() != 4 or k.dim() != 4 or k_cache.dim() != 4:
+        return "q, k and k_cache must be 4-D"
+    batch, seq, _, head_dim = q.shape
+    kv_heads = k.shape[2]
+    if tuple(k.shape) != (batch, seq, kv_heads, head_dim) or k.dtype != q.dtype:
+        return f"k {tuple(k.shape)} {k.dtype} does not match q {tuple(q.shape)} {q.dtype}"
+    if (tuple(k_cache.shape) != (batch, kv_heads, k_cache.shape[2], head_dim)
+            or k_cache.dtype != q.dtype):
+        return (f"k_cache {tuple(k_cache.shape)} {k_cache.dtype} is not "
+                f"(batch, kv_heads, cache_len, head_dim) of {q.dtype}")
+    if (v is None) != (v_cache is None):
+        return "v and v_cache must both be given or both be None"
+    if v is not None and (tuple(v.shape) != tuple(k.shape) or v.dtype != q.dtype
+                          or tuple(v_cache.shape) != tuple(k_cache.shape) or v_cache.dtype != q.dtype
+                          or v_cache.stride() != k_cache.stride()):
+        return "v / v_cache must match k / k_cache (shapes, dtype, strides)"
+    if cos.dim() != 2 or cos.shape[1] != head_dim // 2 or sin.shape != cos.shape:
+        return f"tables must be (positions, {head_dim // 2}), got {tuple(cos.shape)}"
+    if pos.dtype != torch.int64 or pos.numel() < 1:
+        return "pos must be an int64 tensor holding the position"
+    index = q.get_device()
+    for name, t in (("k", k), ("k_cache", k_cache), ("pos", pos)) + (
+            (("v", v), ("v_cache", v_cache)) if v is not None else ()):
+        if not t.is_cuda or t.get_device() != index:
+            return f"{name} must be on the device of q"
+    if k_cache.stride(-1) != 1 or (v_cache is not None and v_cache.stride(-1) != 1):
+        return "cache rows must be contiguous in head_dim"
+    return "unsupported arguments"
 
 
 def rope_qk_cache_hip(
@@ -127,56 +165,60 @@ def rope_qk_cache_hip(
     be captured in a HIP graph while the position advances between replays.
     Tokens whose slot falls outside the cache are not written (the host
     cannot see ``pos`` without a synchronisation); callers keep
-    ``pos + seq <= cache_len``.
+    ``pos + seq <= cache_len``. This runs once per layer and decode step, so
+    the common case is checked with one combined test and the detailed
+    message is only built when it fails.
     """
     index = gpu_index(q, "rope_qk_cache_hip")
-    if q.dim() != 4 or k.dim() != 4 or k_cache.dim() != 4:
-        raise ValueError("rope_qk_cache_hip: q, k and k_cache must be 4-D")
-    batch, seq, q_heads, head_dim = q.shape
-    kv_heads = k.shape[2]
-    cache_len = k_cache.shape[2]
-    if style not in _native.ROPE_STYLE_CODES:
-        raise ValueError(f"Unknown RoPE style {style!r}")
-    if tuple(k.shape) != (batch, seq, kv_heads, head_dim) or k.dtype != q.dtype:
-        raise ValueError(f"rope_qk_cache_hip: k {tuple(k.shape)} {k.dtype} does not match q {tuple(q.shape)} {q.dtype}")
-    if tuple(k_cache.shape) != (batch, kv_heads, cache_len, head_dim) or k_cache.dtype != q.dtype:
-        raise ValueError(f"rope_qk_cache_hip: k_cache {tuple(k_cache.shape)} {k_cache.dtype} is not "
-                         f"(batch, kv_heads, cache_len, head_dim) of {q.dtype}")
-    if (v is None) != (v_cache is None):
-        raise ValueError("rope_qk_cache_hip: v and v_cache must both be given or both be None")
-    if v is not None and (tuple(v.shape) != tuple(k.shape) or v.dtype != q.dtype
-                          or tuple(v_cache.shape) != tuple(k_cache.shape) or v_cache.dtype != q.dtype
-                          or v_cache.stride() != k_cache.stride()):
-        raise ValueError("rope_qk_cache_hip: v / v_cache must match k / k_cache (shapes, dtype, strides)")
-    if cos.dim() != 2 or cos.shape[1] != head_dim // 2 or sin.shape != cos.shape:
-        raise ValueError(f"rope_qk_cache_hip: tables must be (positions, {head_dim // 2}), got {tuple(cos.shape)}")
-    if pos.dtype != torch.int64 or pos.numel() < 1:
-        raise ValueError("rope_qk_cache_hip: pos must be an int64 tensor holding the position")
-    for name, t in (("k", k), ("k_cache", k_cache), ("pos", pos)) + (
-            (("v", v), ("v_cache", v_cache)) if v is not None else ()):
-        if not t.is_cuda or t.get_device() != index:
-            raise ValueError(f"rope_qk_cache_hip: {name} must be on the device of q")
-    if k_cache.stride(-1) != 1 or (v_cache is not None and v_cache.stride(-1) != 1):
-        raise ValueError("rope_qk_cache_hip: cache rows must be contiguous in head_dim")
-    dt = dtype_code(q.dtype, "rope_qk_cache_hip")
+    style_code = _native.ROPE_STYLE_CODES.get(style)
+    qshape, kshape, cshape = q.shape, k.shape, k_cache.shape
+    dt = DT.get(q.dtype)
+    ok = (
+        style_code is not None and dt is not None and len(qshape) == 4 and len(kshape) == 4
+        and len(cshape) == 4 and kshape[0] == qshape[0] and kshape[1] == qshape[1]
+        and kshape[3] == qshape[3] and cshape[0] == qshape[0] and cshape[1] == kshape[2]
+        and cshape[3] == qshape[3] and k.dtype is q.dtype and k_cache.dtype is q.dtype
+        and cos.dim() == 2 and cos.shape[1] * 2 == qshape[3] and sin.shape == cos.shape
+        and pos.dtype is torch.int64 and pos.numel() >= 1 and k.is_cuda and k_cache.is_cuda and pos.is_cuda
+        and k_cache.stride(3) == 1
+    )
+    if ok and v is not None:
+        ok = (v_cache is not None and v.shape == kshape and v.dtype is q.dtype and v.is_cuda
+              and v_cache.shape == cshape and v_cache.dtype is q.dtype and v_cache.is_cuda
+              and v_cache.stride() == k_cache.stride())
+    elif ok:
+        ok = v_cache is None
+    if not ok or k.get_device() != index or k_cache.get_device() != index or pos.get_device() != index:
+        raise ValueError("rope_qk_cache_hip: " + _cache_args_error(q, k, v, cos, sin, pos, k_cache, v_cache, style))
+    batch, seq, q_heads, head_dim = qshape
     qv, kv = _head_view(q), _head_view(k)
     vv = _head_view(v) if v is not None else None
-    c, s, st = _table_stride(_table(cos, index), _table(sin, index))
-    q_out = torch.empty_like(q) if q.is_contiguous() else torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    qs, ks, qos = qv.stride(), kv.stride(), q_out.stride()
-    vs = vv.stride() if vv is not None else (0, 0, 0, 0)
-    cs = k_cache.stride()
-    strides = _I64x15(qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
-                      qos[0], qos[1], qos[2], cs[0], cs[2], cs[1])
+    tdt = cos.dtype
+    if tdt is sin.dtype and tdt in DT and cos.is_contiguous() and sin.is_contiguous() \
+            and cos.is_cuda and cos.get_device() == index and sin.get_device() == index:
+        c, s, st = cos, sin, cos.shape[1]  # the common case: one dense table pair
+    else:
+        c, s, st = _table_stride(_table(cos, index), _table(sin, index))
+    q_out = torch.empty_like(q) if q.is_contiguous() else torch.empty(qshape, dtype=q.dtype, device=q.device)
+    key = (qv.stride(), kv.stride(), vv.stride() if vv is not None else None, q_out.stride(),
+           k_cache.stride())
+    strides = _strides_cache.get(key)
+    if strides is None:
+        qs, ks, vs, qos, cs = key
+        vs = vs or (0, 0, 0, 0)
+        strides = _I64x15(qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                          qos[0], qos[1], qos[2], cs[0], cs[2], cs[1])
+        if len(_strides_cache) < 256:
+            _strides_cache[key] = strides
     base = _addressof(strides)
     status = call(
         index, lib().ako_rope_qk_cache_fwd,
         qv.data_ptr(), kv.data_ptr(), vv.data_ptr() if vv is not None else None,
         c.data_ptr(), s.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(),
         v_cache.data_ptr() if v_cache is not None else None, pos.data_ptr(),
-        batch, seq, q_heads, kv_heads, head_dim,
+        batch, seq, q_heads, kshape[2], head_dim,
         base, base + 24, base + 48, base + 72, base + 96,
-        cache_len, c.shape[0], st, dt, _native.DTYPE_CODES[c.dtype], _native.ROPE_STYLE_CODES[style],
+        cshape[2], c.shape[0], st, dt, _native.DTYPE_CODES[c.dtype], style_code,
         raw_stream(index),
     )
     if status:
