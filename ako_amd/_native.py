@@ -45,6 +45,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _int,
         [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _ptr],
     ),
+    "ako_rmsnorm_shard_partial_fwd": (_int, [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _int, _ptr]),
+    "ako_rmsnorm_shard_apply_fwd": (
+        _int, [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _ptr],
+    ),
     "ako_rope_fwd": (
         _int,
         [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

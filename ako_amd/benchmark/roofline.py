@@ -57,6 +57,16 @@ def alg_bytes_rope_qk_cache(batch: int, seq: int, q_heads: int, kv_heads: int, h
     return 2 * batch * seq * heads * head_dim * elem_bytes(dtype) + 2 * seq * (head_dim // 2) * elem_bytes(table_dtype)
 
 
+def alg_bytes_rmsnorm_shard_partial(rows: int, shard: int, dtype: torch.dtype, *, residual: bool) -> int:
+    """x (and r) read, s written with a residual; one fp32 partial sum per row."""
+    return (3 if residual else 1) * rows * shard * elem_bytes(dtype) + 4 * rows
+
+
+def alg_bytes_rmsnorm_shard_apply(rows: int, shard: int, dtype: torch.dtype) -> int:
+    """s read, y written, the weight slice and one fp32 total per row read."""
+    return 2 * rows * shard * elem_bytes(dtype) + shard * elem_bytes(dtype) + 4 * rows
+
+
 def alg_bytes_swiglu(rows: int, n: int, dtype: torch.dtype) -> int:
     return 3 * rows * n * elem_bytes(dtype)
 

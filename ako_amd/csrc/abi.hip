@@ -205,6 +205,102 @@ int ako_rmsnorm_residual_fwd(const void* x, const void* residual, const void* w,
                         y_row_stride, rout_row_stride, eps, dtype, w_dtype, stream, true);
 }
 
+// ------------------------------------------- RMSNorm over a sharded row --
+int ako_rmsnorm_shard_partial_fwd(const void* x, const void* residual, void* residual_out,
+                                  float* partial_ss, int64_t rows, int64_t shard,
+                                  int64_t x_row_stride, int64_t r_row_stride,
+                                  int64_t rout_row_stride, int dtype, void* stream) {
+  const char* fn = "ako_rmsnorm_shard_partial_fwd";
+  if (!valid_dtype(dtype)) return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code %d", fn, dtype);
+  if (rows < 0 || shard < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  if (rows == 0) return AKO_OK;
+  if (shard > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: shard=%lld exceeds 2^31-1", fn, (long long)shard);
+  const bool res = residual != nullptr;
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: residual and residual_out must both be given or both be null", fn);
+  if (!partial_ss || (shard > 0 && !x)) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  if (x_row_stride < 0 || (res && (r_row_stride < 0 || rout_row_stride < 0)))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative row stride", fn);
+  if (res && rows > 1 && rout_row_stride < shard)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: residual_out row stride smaller than the shard", fn);
+  const int eb = ako::dtype_bytes(dtype);
+  const Span ps = span_2d(partial_ss, 1, rows, rows, 4);
+  const Span xs = span_2d(x, rows, shard, x_row_stride, eb);
+  if (!ps.ok || !xs.ok) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
+  if (shard > 0 && overlap(ps, xs)) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: partial_ss overlaps x", fn);
+  bool vec = aligned(x, 16) && (x_row_stride * eb) % 16 == 0;
+  if (res) {
+    const Span rs = span_2d(residual, rows, shard, r_row_stride, eb);
+    const Span os = span_2d(residual_out, rows, shard, rout_row_stride, eb);
+    if (!rs.ok || !os.ok) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
+    if (shard > 0 && (overlap(os, xs) || overlap(os, rs) || overlap(os, ps) || overlap(ps, rs)))
+      return fail(AKO_ERR_INVALID_ARGUMENT, "%s: an output overlaps another buffer", fn);
+    vec = vec && aligned(residual, 16) && aligned(residual_out, 16) && (r_row_stride * eb) % 16 == 0 &&
+          (rout_row_stride * eb) % 16 == 0;
+  }
+  ako::RmsShardArgs a{};
+  a.x = x;
+  a.r = residual;
+  a.rout = residual_out;
+  a.partial = partial_ss;
+  a.rows = rows;
+  a.shard = shard;
+  a.sx = x_row_stride;
+  a.sr = r_row_stride;
+  a.srout = rout_row_stride;
+  a.dtype = dtype;
+  a.residual = res;
+  a.vector_ok = vec;
+  return hip_status(ako::launch_rmsnorm_shard_partial(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+int ako_rmsnorm_shard_apply_fwd(const void* s, const void* w, const float* total_ss, void* y,
+                                int64_t rows, int64_t shard, int64_t hidden, int64_t s_row_stride,
+                                int64_t y_row_stride, float eps, int dtype, int w_dtype,
+                                void* stream) {
+  const char* fn = "ako_rmsnorm_shard_apply_fwd";
+  if (!valid_dtype(dtype)) return fail(AKO_ERR_UNSUPPORTED, "%s: unknown dtype code %d", fn, dtype);
+  if (w_dtype != dtype && w_dtype != AKO_DTYPE_F32)
+    return fail(AKO_ERR_UNSUPPORTED, "%s: weight dtype %s with input dtype %s (weight must match or be f32)",
+                fn, dtype_name(w_dtype), dtype_name(dtype));
+  if (rows < 0 || shard < 0 || hidden < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative size", fn);
+  if (rows == 0 || shard == 0) return AKO_OK;
+  if (shard > hidden) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: shard %lld larger than hidden %lld", fn,
+                                  (long long)shard, (long long)hidden);
+  if (shard > kMaxInt) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: shard=%lld exceeds 2^31-1", fn, (long long)shard);
+  if (!s || !w || !total_ss || !y) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: null pointer argument", fn);
+  if (!(eps >= 0.0f)) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: eps must be >= 0", fn);
+  if (s_row_stride < 0 || y_row_stride < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: negative row stride", fn);
+  if (rows > 1 && y_row_stride < shard)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output row stride smaller than the shard", fn);
+  const int eb = ako::dtype_bytes(dtype);
+  const Span ss = span_2d(s, rows, shard, s_row_stride, eb);
+  const Span ys = span_2d(y, rows, shard, y_row_stride, eb);
+  const Span ws = span_2d(w, 1, shard, shard, ako::dtype_bytes(w_dtype));
+  const Span ts = span_2d(total_ss, 1, rows, rows, 4);
+  if (!ss.ok || !ys.ok || !ws.ok || !ts.ok)
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: sizes and strides overflow the address space", fn);
+  if (overlap(ys, ss) || overlap(ys, ws) || overlap(ys, ts))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "%s: output y overlaps an input", fn);
+  const bool vec = aligned(s, 16) && aligned(y, 16) && aligned(w, 16) && (s_row_stride * eb) % 16 == 0 &&
+                   (y_row_stride * eb) % 16 == 0;
+  ako::RmsShardArgs a{};
+  a.x = s;
+  a.w = w;
+  a.total = total_ss;
+  a.y = y;
+  a.rows = rows;
+  a.shard = shard;
+  a.hidden = hidden;
+  a.sx = s_row_stride;
+  a.sy = y_row_stride;
+  a.eps = eps;
+  a.dtype = dtype;
+  a.w_dtype = w_dtype;
+  a.vector_ok = vec;
+  return hip_status(ako::launch_rmsnorm_shard_apply(a, static_cast<hipStream_t>(stream)), fn);
+}
+
 // ------------------------------------------------------------------- RoPE --
 namespace {
 

@@ -52,6 +52,30 @@ struct RmsArgs {
 };
 hipError_t launch_rmsnorm(const RmsArgs& a, hipStream_t stream);
 
+// One rank's slice of a hidden-sharded row (tensor parallelism). partial:
+// x (+ r, rounded, to rout) -> fp32 sum of squares per row in `partial`.
+// apply: x holds s, `total` the all-reduced sums, y = s * rsqrt(total/H + eps) * w.
+struct RmsShardArgs {
+  const void* x;
+  const void* r;
+  const void* w;
+  void* y;
+  void* rout;
+  float* partial;
+  const float* total;
+  int64_t rows;
+  int64_t shard;   // elements of the slice
+  int64_t hidden;  // full row length H (apply)
+  int64_t sx, sr, sy, srout;
+  float eps;
+  int dtype;
+  int w_dtype;
+  bool residual;
+  bool vector_ok;
+};
+hipError_t launch_rmsnorm_shard_partial(const RmsShardArgs& a, hipStream_t stream);
+hipError_t launch_rmsnorm_shard_apply(const RmsShardArgs& a, hipStream_t stream);
+
 struct RopeTensorArgs {
   const void* x;
   void* y;

@@ -268,6 +268,79 @@ __global__ __launch_bounds__(kStreamBlock) void rmsnorm_stream(
   }
 }
 
+// Tensor-parallel halves of (residual) RMSNorm, for a row whose hidden
+// dimension is split over ranks. Each rank runs rmsnorm_shard_partial on its
+// slice (s = x (+ r), rounded to T and written when there is a residual, and
+// the fp32 sum of squares of s), the partial sums are all-reduced across the
+// ranks, and rmsnorm_shard_apply normalises each slice with the total:
+//   y = to_T((s * rsqrt(total * (1/H) + eps)) * w)
+// with H the full hidden size, the same arithmetic as rmsnorm_reg. One
+// 256-lane workgroup per row, packets of E elements (E = 1 when unaligned).
+template <typename T, int E, bool RES>
+__global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_partial(
+    const T* __restrict__ x, const T* __restrict__ res, T* __restrict__ rout,
+    float* __restrict__ partial, int64_t row0, int shard, int64_t sx, int64_t sr, int64_t srout) {
+  using P = Pack<T, E>;
+  const int64_t row = row0 + blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = shard / E;
+  const T* xr = x + row * sx;
+  float ss = 0.f;
+  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
+    P p = load_pack<T, E, true>(xr + vi * E);
+    if constexpr (RES) {
+      const P q = load_pack<T, E, true>(res + row * sr + vi * E);
+#pragma unroll
+      for (int e = 0; e < E; ++e) p.e[e] = from_f32<T>(to_f32(p.e[e]) + to_f32(q.e[e]));
+      store_pack<T, E, true>(rout + row * srout + vi * E, p);
+    }
+    ss = sumsq_add(p, ss);
+  }
+  for (int j = nvec * E + tid; j < shard; j += kStreamBlock) {  // tail (E > 1 only)
+    T v = xr[j];
+    if constexpr (RES) {
+      v = from_f32<T>(to_f32(v) + to_f32(res[row * sr + j]));
+      rout[row * srout + j] = v;
+    }
+    const float f = to_f32(v);
+    ss = __builtin_fmaf(f, f, ss);
+  }
+  ss = wave_sum(ss);
+  __shared__ float lds[kStreamBlock / kWave];
+  if ((tid & (kWave - 1)) == 0) lds[tid / kWave] = ss;
+  __syncthreads();
+  if (tid == 0) {
+    float total = 0.f;
+#pragma unroll
+    for (int j = 0; j < kStreamBlock / kWave; ++j) total += lds[j];
+    partial[row] = total;
+  }
+}
+
+template <typename T, typename W, int E>
+__global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_apply(
+    const T* __restrict__ s, const W* __restrict__ w, const float* __restrict__ total,
+    T* __restrict__ y, int64_t row0, int shard, int64_t ss_, int64_t sy, float inv_h, float eps) {
+  using P = Pack<T, E>;
+  const int64_t row = row0 + blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = shard / E;
+  const float rstd = rsqrtf(total[row] * inv_h + eps);
+  const T* sr = s + row * ss_;
+  T* yr = y + row * sy;
+  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
+    const P p = load_pack<T, E, true>(sr + vi * E);
+    float wf[E];
+    load_f32<W, E>(w + vi * E, wf);
+    P o;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(p.e[e]) * rstd) * wf[e]);
+    store_pack<T, E, true>(yr + vi * E, o);
+  }
+  for (int j = nvec * E + tid; j < shard; j += kStreamBlock)
+    yr[j] = from_f32<T>((to_f32(sr[j]) * rstd) * to_f32(w[j]));
+}
+
 #ifndef AKO_RMS_NT
 #define AKO_RMS_NT 1
 #endif
@@ -429,6 +502,74 @@ hipError_t run_typed(const RmsArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+namespace {
+
+template <typename T, bool RES>
+hipError_t run_shard_partial(const RmsShardArgs& a, hipStream_t stream) {
+  const int64_t cap = max_blocks_per_launch(kStreamBlock);
+  for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
+    const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
+    if (a.vector_ok) {
+      hipLaunchKernelGGL((rmsnorm_shard_partial<T, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
+                         stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                         static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
+                         a.sr, a.srout);
+    } else {
+      hipLaunchKernelGGL((rmsnorm_shard_partial<T, 1, RES>), grid, dim3(kStreamBlock), 0, stream,
+                         static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                         static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
+                         a.sr, a.srout);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+template <typename T, typename W>
+hipError_t run_shard_apply(const RmsShardArgs& a, hipStream_t stream) {
+  const int64_t cap = max_blocks_per_launch(kStreamBlock);
+  const float inv_h = 1.0f / static_cast<float>(a.hidden);
+  for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
+    const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
+    if (a.vector_ok) {
+      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 16 / sizeof(T)>), grid, dim3(kStreamBlock), 0,
+                         stream, static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
+                         static_cast<T*>(a.y), r0, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                         a.eps);
+    } else {
+      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 1>), grid, dim3(kStreamBlock), 0, stream,
+                         static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
+                         static_cast<T*>(a.y), r0, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                         a.eps);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_shard_partial(const RmsShardArgs& a, hipStream_t stream) {
+  switch (a.dtype) {
+    case kF32: return a.residual ? run_shard_partial<float, true>(a, stream) : run_shard_partial<float, false>(a, stream);
+    case kF16: return a.residual ? run_shard_partial<_Float16, true>(a, stream) : run_shard_partial<_Float16, false>(a, stream);
+    case kBF16: return a.residual ? run_shard_partial<__bf16, true>(a, stream) : run_shard_partial<__bf16, false>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rmsnorm_shard_apply(const RmsShardArgs& a, hipStream_t stream) {
+  const bool w_same = a.w_dtype == a.dtype;
+  switch (a.dtype) {
+    case kF32: return run_shard_apply<float, float>(a, stream);
+    case kF16: return w_same ? run_shard_apply<_Float16, _Float16>(a, stream) : run_shard_apply<_Float16, float>(a, stream);
+    case kBF16: return w_same ? run_shard_apply<__bf16, __bf16>(a, stream) : run_shard_apply<__bf16, float>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_rmsnorm(const RmsArgs& a, hipStream_t stream) {
   const bool w_same = a.w_dtype == a.dtype;

@@ -174,6 +174,25 @@ def main() -> int:
         cells.append(("rope_qk_cache_fp16_1x1_q32_kv32_slot511of640", cache_bytes,
                       lambda: rope_qk_cache_hip(q1, k1, v1, full_cos, full_sin, pos, kc, vc, "neox")))
         cells.append(("rope_qk_then_index_copy_fp16_1x1_q32_kv32", cache_bytes, unfused_cache_step))
+        # One tensor-parallel rank's slice of the widest configs[1] row (TP=8:
+        # 2048 of 16384): residual + partial sum of squares, then the apply half.
+        from ako_amd.ops.rmsnorm_tp import rmsnorm_shard_apply_hip, rmsnorm_shard_partial_hip
+
+        for dtype in (torch.float16, torch.bfloat16):
+            tag = "fp16" if dtype == torch.float16 else "bf16"
+            rows_tp, shard = RMS_ROWS, 2048
+            nb_p = rf.alg_bytes_rmsnorm_shard_partial(rows_tp, shard, dtype, residual=True)
+            nb_a = rf.alg_bytes_rmsnorm_shard_apply(rows_tp, shard, dtype)
+            copies = rf.copies_for_cold(nb_p, dev)
+            xs_tp = [rnd(rows_tp, shard, dtype=dtype) for _ in range(copies)]
+            rs_tp = [rnd(rows_tp, shard, dtype=dtype) for _ in range(copies)]
+            w_tp = rnd(shard, dtype=dtype, scale=0.1, shift=1.0)
+            tot = torch.full((rows_tp,), float(shard), device=dev)
+            for i in range(copies):
+                cells.append((f"rmsnorm_shard_partial_{tag}_{rows_tp}x{shard}_residual", nb_p,
+                              lambda x=xs_tp[i], r=rs_tp[i]: rmsnorm_shard_partial_hip(x, r)))
+                cells.append((f"rmsnorm_shard_apply_{tag}_{rows_tp}x{shard}", nb_a,
+                              lambda s_=xs_tp[i]: rmsnorm_shard_apply_hip(s_, w_tp, tot, 8 * shard, 1e-6)))
         for m in (16384, 4096, 256, 16, 1):
             dtype = torch.bfloat16
             nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)

@@ -94,6 +94,30 @@ int ako_rmsnorm_residual_fwd(const void* x, const void* residual, const void* w,
                              float eps, int dtype, int w_dtype, void* stream);
 
 /*
+ * RMSNorm of a row whose hidden dimension is split over tensor-parallel
+ * ranks: the per-rank halves of a fused all-reduce + residual + RMSNorm. The
+ * reference has no tensor parallelism, so neither has a counterpart there;
+ * together they compute rmsnorm_residual_ref / rmsnorm_ref
+ * (ako/ops/rmsnorm_ref.py:8-50) on the whole row, up to the order of the
+ * fp32 sum of squares:
+ *   partial:  s = x (+ residual, rounded to dtype, written to residual_out;
+ *             both NULL for plain RMSNorm), partial_ss[row] = sum of s^2 over
+ *             the rank's `shard` elements (fp32);
+ *   (the caller sums partial_ss over the ranks, e.g. one all-reduce)
+ *   apply:    y = to_dtype((s * rsqrt(total_ss[row] * (1/hidden) + eps)) * w)
+ *             on the rank's slice, with `hidden` the full row length.
+ * Row strides in elements; partial_ss / total_ss hold `rows` floats.
+ */
+int ako_rmsnorm_shard_partial_fwd(const void* x, const void* residual, void* residual_out,
+                                  float* partial_ss, int64_t rows, int64_t shard,
+                                  int64_t x_row_stride, int64_t r_row_stride,
+                                  int64_t rout_row_stride, int dtype, void* stream);
+int ako_rmsnorm_shard_apply_fwd(const void* s, const void* w, const float* total_ss, void* y,
+                                int64_t rows, int64_t shard, int64_t hidden,
+                                int64_t s_row_stride, int64_t y_row_stride, float eps,
+                                int dtype, int w_dtype, void* stream);
+
+/*
  * Rotary position embedding of x[batch, seq, heads, head_dim]:
  *   for each pair (a, b) of a head at position s, with c = cos[s, i],
  *   n = sin[s, i]:   a' = a*c - b*n,   b' = a*n + b*c     (fp32)
