@@ -23,7 +23,8 @@ import torch
 
 from ako_amd.benchmark import roofline as rf
 from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
-from ako_amd.ops.rope_hip import rope_hip, rope_qk_hip
+from ako_amd.ops.rmsnorm_tp import rmsnorm_shard_apply_hip, rmsnorm_shard_partial_hip
+from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
 from ako_amd.ops.rope_ref import build_rope_tables
 from ako_amd.ops.swiglu_hip import swiglu_hip
 
@@ -52,6 +53,23 @@ def build(device: torch.device):
                       lambda q=q, c=cos, s=sin: rope_hip(q, c, s)))
         cells.append((f"rope_qk_{tag}_4x2048", rf.alg_bytes_rope(4, 2048, 40, 128, dtype, dtype),
                       lambda q=q, k=k, c=cos, s=sin: rope_qk_hip(q, k, c, s)))
+        # q, k and v of a 2048-token prefill into a heads-major KV cache at slot 0.
+        v = rnd(4, 2048, 8, 128, dtype=dtype)
+        kc, vc = rnd(4, 8, 2048, 128, dtype=dtype), rnd(4, 8, 2048, 128, dtype=dtype)
+        pos = torch.zeros(1, dtype=torch.long, device=device)
+        cells.append((f"rope_qk_cache_{tag}_4x2048_q32_kv8",
+                      rf.alg_bytes_rope_qk_cache(4, 2048, 32, 8, 128, dtype, dtype),
+                      lambda q=q, k=k, v=v, c=cos, s=sin, kc=kc, vc=vc, p=pos:
+                      rope_qk_cache_hip(q, k, v, c, s, p, kc, vc)))
+        # One TP=8 rank's slice of the widest configs[1] row.
+        xs, rs = rnd(16384, 2048, dtype=dtype), rnd(16384, 2048, dtype=dtype)
+        ws = rnd(2048, dtype=dtype, scale=0.1, shift=1.0)
+        total = torch.full((16384,), 2048.0, device=device)
+        cells.append((f"rmsnorm_shard_partial_{tag}_16384x2048_residual",
+                      rf.alg_bytes_rmsnorm_shard_partial(16384, 2048, dtype, residual=True),
+                      lambda x=xs, r=rs: rmsnorm_shard_partial_hip(x, r)))
+        cells.append((f"rmsnorm_shard_apply_{tag}_16384x2048", rf.alg_bytes_rmsnorm_shard_apply(16384, 2048, dtype),
+                      lambda x=xs, w=ws, t=total: rmsnorm_shard_apply_hip(x, w, t, 16384, 1e-6)))
     g, u = rnd(16384, 14336, dtype=torch.bfloat16), rnd(16384, 14336, dtype=torch.bfloat16)
     cells.append(("swiglu_bf16_16384x14336", rf.alg_bytes_swiglu(16384, 14336, torch.bfloat16),
                   lambda g=g, u=u: swiglu_hip(g, u)))

@@ -49,7 +49,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decoder", action="store_true", help="skip the configs[4] decoder run")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "traffic_config2_rope_swiglu.md",
+    ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "hbm_traffic_hot_path_cells.md",
                     help="rocprofv3 FETCH/WRITE summary (ako_amd.benchmark.rocprof) for the kernels")
     return ap.parse_args()
 
