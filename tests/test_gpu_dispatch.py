@@ -132,10 +132,11 @@ def test_cache_rope_graph_follows_the_device_position() -> None:
     assert not kc[:, :, :start].any() and not kc[:, :, start + 6:].any()
 
 
-def test_decoder_backends_agree_on_gpu() -> None:
+@pytest.mark.parametrize("n_kv_heads", [4, 2])
+def test_decoder_backends_agree_on_gpu(n_kv_heads: int) -> None:
     from ako_amd.models.decoder import ModelConfig, build_lm
 
-    cfg = ModelConfig(hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=4, intermediate_dim=1024,
+    cfg = ModelConfig(hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=n_kv_heads, intermediate_dim=1024,
                       max_seq_len=96, vocab_size=1000, eps=1e-6)
     prompt = torch.randint(0, 1000, (1, 33), generator=torch.Generator().manual_seed(0)).to(DEV)
     outs = {}
@@ -150,10 +151,11 @@ def test_decoder_backends_agree_on_gpu() -> None:
         assert (a - b).abs().max().item() <= 2e-2 * b.abs().max().item() + 1e-3
 
 
-def test_graphed_greedy_matches_eager_static_decoding() -> None:
+@pytest.mark.parametrize("n_kv_heads", [4, 2])
+def test_graphed_greedy_matches_eager_static_decoding(n_kv_heads: int) -> None:
     from ako_amd.models.decoder import GraphedGreedy, ModelConfig, build_lm
 
-    cfg = ModelConfig(hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=4, intermediate_dim=1024,
+    cfg = ModelConfig(hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=n_kv_heads, intermediate_dim=1024,
                       max_seq_len=64, vocab_size=1000, eps=1e-6)
     prompt = torch.randint(0, 1000, (1, 17), generator=torch.Generator().manual_seed(1)).to(DEV)
     for backend in ("ako", "torch"):
