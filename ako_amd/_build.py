@@ -102,6 +102,54 @@ def build_library(*, verbose: bool = False, extra_flags: list[str] | None = None
     return out
 
 
+BINDING_SOURCE = CSRC / "torch_bind.cpp"
+
+
+def binding_path() -> Path:
+    import sysconfig
+
+    return LIB_DIR / ("_ako_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_torch_binding(*, verbose: bool = False) -> Path:
+    """Compile the PyTorch binding (``_ako_torch``, host code only, g++).
+
+    It links ``libako_hip.so`` from the same directory (rpath ``$ORIGIN``)
+    and torch's libraries; the HIP headers are needed only for torch's HIP
+    stream API. Build the kernel library first.
+    """
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} must be built before the torch binding")
+    try:
+        includes = cpp_extension.include_paths(device_type="cuda")
+    except TypeError:  # older signature
+        includes = cpp_extension.include_paths(cuda=True)
+    tlib = torch_lib_dir()
+    out = binding_path()
+    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+    abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
+    cmd = [
+        shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+        "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_ako_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-I{INCLUDE}", f"-I{sysconfig.get_paths()['include']}",
+        *(f"-I{p}" for p in includes), "-I/opt/rocm/include",
+        str(BINDING_SOURCE), "-o", str(tmp),
+        f"-L{LIB_DIR}", "-lako_hip", "-Wl,-rpath,$ORIGIN",
+        f"-L{tlib}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+        "-lamdhip64", f"-Wl,-rpath,{tlib}",
+    ]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
+    print(build_torch_binding(verbose="-v" in sys.argv))

@@ -131,6 +131,48 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_binding: Any = None
+_binding_checked = False
+
+
+def torch_binding() -> Any:
+    """The PyTorch binding module ``_ako_torch`` (built next to the library by
+    ``ako_amd._build.build_torch_binding``), or ``None`` when it is not built
+    or ``AKO_TORCH_BINDING=0``.
+
+    It does each HIP candidate's host work (checks, allocation, stream) in
+    C++ and calls the same C ABI; without it the candidates make the same
+    calls through ctypes. Both launch the same kernels of this library: the
+    binding is a faster host path, never a different compute path. Loading
+    it loads (and checks) the kernel library first.
+    """
+    global _binding, _binding_checked
+    if _binding_checked:
+        return _binding
+    _binding_checked = True
+    if os.environ.get("AKO_TORCH_BINDING", "1").strip() == "0":
+        return None
+    load()
+    import importlib.util
+    import logging
+    import sysconfig
+
+    path = library_path().with_name("_ako_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not path.exists():
+        return None
+    try:
+        spec = importlib.util.spec_from_file_location("_ako_torch", path)
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+    except ImportError as exc:
+        logging.getLogger(__name__).warning("torch binding %s not usable (%s); using ctypes", path, exc)
+        return None
+    if module.abi_version() != ABI_VERSION:
+        raise HipLibraryError(f"{path} was built for ABI {module.abi_version()}, need {ABI_VERSION}; rebuild")
+    _binding = module
+    return module
+
+
 def is_available() -> bool:
     try:
         load()

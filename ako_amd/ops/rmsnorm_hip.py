@@ -34,6 +34,14 @@ def _weight(weight: torch.Tensor, index: int, dt: int, hidden: int, fn_name: str
 
 def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """RMSNorm over the last dimension on the GPU."""
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.rmsnorm(x, weight, eps)
+    return rmsnorm_hip_ctypes(x, weight, eps)
+
+
+def rmsnorm_hip_ctypes(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``rmsnorm_hip`` with the host work in Python and the call through ctypes."""
     index = gpu_index(x, "rmsnorm_hip")
     dt = dtype_code(x.dtype, "rmsnorm_hip")
     hidden = x.shape[-1] if x.dim() else 1
@@ -52,6 +60,16 @@ def rmsnorm_residual_hip(
     x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``(rmsnorm(x + residual), x + residual)`` with the sum rounded to x's dtype."""
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.rmsnorm_residual(x, residual, weight, eps)
+    return rmsnorm_residual_hip_ctypes(x, residual, weight, eps)
+
+
+def rmsnorm_residual_hip_ctypes(
+    x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``rmsnorm_residual_hip`` with the host work in Python and the call through ctypes."""
     index = gpu_index(x, "rmsnorm_residual_hip")
     if x.shape != residual.shape:
         raise ValueError(f"Shape mismatch: x {tuple(x.shape)} vs residual {tuple(residual.shape)}")

@@ -46,6 +46,16 @@ def _table_stride(cos: torch.Tensor, sin: torch.Tensor) -> tuple[torch.Tensor, t
 def rope_hip(
     x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
 ) -> torch.Tensor:
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.rope(x, cos, sin, style)
+    return rope_hip_ctypes(x, cos, sin, style)
+
+
+def rope_hip_ctypes(
+    x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
+) -> torch.Tensor:
+    """``rope_hip`` with the host work in Python and the call through ctypes."""
     index = gpu_index(x, "rope_hip")
     validate_rope_args(x, cos, sin, style)
     dt = dtype_code(x.dtype, "rope_hip")
@@ -75,6 +85,16 @@ def rope_qk_hip(
     q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Rotate ``q`` and ``k`` (same batch, seq, head_dim and dtype) in one launch."""
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.rope_qk(q, k, cos, sin, style)
+    return rope_qk_hip_ctypes(q, k, cos, sin, style)
+
+
+def rope_qk_hip_ctypes(
+    q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, style: str = "neox"
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``rope_qk_hip`` with the host work in Python and the call through ctypes."""
     index = gpu_index(q, "rope_qk_hip")
     validate_rope_args(q, cos, sin, style)
     validate_rope_args(k, cos, sin, style)
@@ -165,10 +185,28 @@ def rope_qk_cache_hip(
     be captured in a HIP graph while the position advances between replays.
     Tokens whose slot falls outside the cache are not written (the host
     cannot see ``pos`` without a synchronisation); callers keep
-    ``pos + seq <= cache_len``. This runs once per layer and decode step, so
-    the common case is checked with one combined test and the detailed
-    message is only built when it fails.
+    ``pos + seq <= cache_len``.
     """
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.rope_qk_cache(q, k, v, cos, sin, pos, k_cache, v_cache, style)
+    return rope_qk_cache_hip_ctypes(q, k, v, cos, sin, pos, k_cache, v_cache, style)
+
+
+def rope_qk_cache_hip_ctypes(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor | None,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    pos: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor | None,
+    style: str = "neox",
+) -> torch.Tensor:
+    """``rope_qk_cache_hip`` with the host work in Python and the call through
+    ctypes. The common case is checked with one combined test and the detailed
+    message is only built when it fails."""
     index = gpu_index(q, "rope_qk_cache_hip")
     style_code = _native.ROPE_STYLE_CODES.get(style)
     qshape, kshape, cshape = q.shape, k.shape, k_cache.shape

@@ -14,6 +14,14 @@ from ako_amd.ops._hip_common import call, dtype_code, empty_out, gpu_index, lib,
 
 
 def swiglu_hip(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    fast = _native.torch_binding()
+    if fast is not None:
+        return fast.swiglu(gate, up)
+    return swiglu_hip_ctypes(gate, up)
+
+
+def swiglu_hip_ctypes(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``swiglu_hip`` with the host work in Python and the call through ctypes."""
     index = gpu_index(gate, "swiglu_hip")
     if gate.shape != up.shape:
         raise ValueError(f"Shape mismatch: gate {tuple(gate.shape)} vs up {tuple(up.shape)}")

@@ -45,8 +45,13 @@ def compare_reports(
 
 
 def _last_json_line(text: str) -> dict[str, Any]:
-    lines = [ln for ln in text.strip().splitlines() if ln.strip().startswith("{")]
-    return json.loads(lines[-1])
+    """A whole JSON document, or else the last line of a log that is one
+    (``bench.py`` prints its record as the last line of its output)."""
+    try:
+        return json.loads(text)
+    except json.JSONDecodeError:
+        lines = [ln for ln in text.strip().splitlines() if ln.strip().startswith("{")]
+        return json.loads(lines[-1])
 
 
 def compare_bench_lines(

@@ -208,3 +208,28 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path) -> None:
     with pytest.raises(_native.HipLibraryError, match="not built"):
         _native.load()
     assert not _native.is_available()
+
+
+def test_torch_binding_loads_and_checks_like_the_python_wrappers() -> None:
+    """The PyTorch binding (``_ako_torch``) is built next to the library, has the
+    library's ABI, and rejects what the Python wrappers reject, with the same
+    exception type and message (the checks run before any GPU call)."""
+    from ako_amd.ops import rmsnorm_hip, rope_hip, swiglu_hip
+
+    fast = _native.torch_binding()
+    assert fast is not None and fast.abi_version() == _native.ABI_VERSION
+    x, w = torch.zeros(2, 8), torch.ones(8)
+    cases = [
+        (lambda: fast.rmsnorm(x, w, 1e-6), lambda: rmsnorm_hip.rmsnorm_hip_ctypes(x, w, 1e-6)),
+        (lambda: fast.rmsnorm_residual(x, x, w, 1e-6), lambda: rmsnorm_hip.rmsnorm_residual_hip_ctypes(x, x, w)),
+        (lambda: fast.swiglu(x, x), lambda: swiglu_hip.swiglu_hip_ctypes(x, x)),
+        (lambda: fast.rope(x.view(1, 2, 1, 8), w[:4].view(1, 4).expand(2, 4), w[:4].view(1, 4).expand(2, 4), "neox"),
+         lambda: rope_hip.rope_hip_ctypes(x.view(1, 2, 1, 8), w[:4].view(1, 4).expand(2, 4),
+                                          w[:4].view(1, 4).expand(2, 4), "neox")),
+    ]
+    for fast_call, slow_call in cases:
+        with pytest.raises(ValueError) as a:
+            fast_call()
+        with pytest.raises(ValueError) as b:
+            slow_call()
+        assert str(a.value) == str(b.value) and "GPU tensor" in str(a.value)

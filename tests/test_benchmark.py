@@ -150,6 +150,9 @@ def test_bench_line_regression_diff(tmp_path) -> None:
     cur.write_text(json.dumps(_bench_line(value=5000.0)) + "\n")
     assert regression.main([str(cur), str(old)]) == 1
     assert regression.main([str(old), str(old)]) == 0
+    pretty = tmp_path / "pretty.json"  # an indented record, as committed under reports/
+    pretty.write_text(json.dumps(base, indent=1))
+    assert regression.main([str(old), str(pretty)]) == 0
 
 
 def test_graph_capture_is_a_noop_on_cpu() -> None:

@@ -172,3 +172,52 @@ def test_graphed_greedy_matches_eager_static_decoding(n_kv_heads: int) -> None:
                 graphed = GraphedGreedy(model, prompt, 12).run()
                 torch.cuda.synchronize()
                 assert torch.equal(graphed, eager_tokens), (backend, graphed, eager_tokens)
+
+
+def test_torch_binding_matches_the_ctypes_path() -> None:
+    """The C++ binding and the ctypes path launch the same kernels: identical
+    outputs, the same errors, and torch's current stream (side streams too)."""
+    from ako_amd import _native
+    from ako_amd.ops import rmsnorm_hip as rm, rope_hip as rp, swiglu_hip as sw
+
+    fast = _native.torch_binding()
+    assert fast is not None
+    x, r = _rand(33, 4096, seed=40), _rand(33, 4096, seed=41)
+    w = _rand(4096, seed=42, scale=0.1, shift=1.0)
+    q, k, v = _rand(2, 5, 8, 128, seed=43), _rand(2, 5, 2, 128, seed=44), _rand(2, 5, 2, 128, seed=45)
+    cos, sin = build_rope_tables(16, 128, device=DEV)
+    g, u = _rand(7, 1000, seed=46), _rand(7, 1000, seed=47)
+    assert torch.equal(fast.rmsnorm(x, w, 1e-6), rm.rmsnorm_hip_ctypes(x, w, 1e-6))
+    for a, b in zip(fast.rmsnorm_residual(x, r, w, 1e-6), rm.rmsnorm_residual_hip_ctypes(x, r, w, 1e-6)):
+        assert torch.equal(a, b)
+    assert torch.equal(fast.rope(q, cos[:5], sin[:5], "interleaved"), rp.rope_hip_ctypes(q, cos[:5], sin[:5], "interleaved"))
+    for a, b in zip(fast.rope_qk(q, k, cos[:5], sin[:5], "neox"), rp.rope_qk_hip_ctypes(q, k, cos[:5], sin[:5], "neox")):
+        assert torch.equal(a, b)
+    pos = torch.full((1,), 3, dtype=torch.long, device=DEV)
+    caches = [torch.zeros(2, 2, 16, 128, device=DEV, dtype=torch.bfloat16) for _ in range(4)]
+    qa = fast.rope_qk_cache(q, k, v, cos, sin, pos, caches[0], caches[1], "neox")
+    qb = rp.rope_qk_cache_hip_ctypes(q, k, v, cos, sin, pos, caches[2], caches[3], "neox")
+    assert torch.equal(qa, qb) and torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    assert torch.equal(fast.swiglu(g, u), sw.swiglu_hip_ctypes(g, u))
+    bad = [
+        (lambda: fast.rmsnorm(x, w[:100], 1e-6), lambda: rm.rmsnorm_hip_ctypes(x, w[:100], 1e-6)),
+        (lambda: fast.rope(q, cos, sin, "neox"), lambda: rp.rope_hip_ctypes(q, cos, sin, "neox")),
+        (lambda: fast.rope(q, cos[:5], sin[:5], "rot"), lambda: rp.rope_hip_ctypes(q, cos[:5], sin[:5], "rot")),
+        (lambda: fast.rope_qk_cache(q, k, v, cos, sin, pos.int(), caches[0], caches[1], "neox"),
+         lambda: rp.rope_qk_cache_hip_ctypes(q, k, v, cos, sin, pos.int(), caches[0], caches[1], "neox")),
+        (lambda: fast.swiglu(g, u[:3]), lambda: sw.swiglu_hip_ctypes(g, u[:3])),
+    ]
+    for fast_call, slow_call in bad:
+        with pytest.raises(ValueError) as ea:
+            fast_call()
+        with pytest.raises(ValueError) as eb:
+            slow_call()
+        assert str(ea.value) == str(eb.value)
+    assert fast.current_stream(0) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert fast.current_stream(0) == side.cuda_stream
+        y_side = fast.rmsnorm(x, w, 1e-6)
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(y_side, rm.rmsnorm_hip_ctypes(x, w, 1e-6))
