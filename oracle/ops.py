@@ -21,6 +21,10 @@ oracle function      reference                                   pinned by
 ``rope``             ``ako/ops/rope_ref.py:73-107``              manual rotation; pair-norm preservation;
                                                                  position-0 identity; relative-position
                                                                  dot product
+``rope_qk_cache``    ``ako/models/decoder.py:173-177`` (rope of  element-by-element float64 brute force of
+                     q and k, then the cache append of           slot placement, table row and rotation;
+                     ``:84-93``), heads-major cache              out-of-range slots dropped; planted
+                                                                 wrong-slot / wrong-row mistakes caught
 ``swiglu``           ``ako/ops/swiglu_ref.py:16-32``             zero-up -> 0; silu closed form in fp64;
                                                                  first-order error bound
 ===================  ==========================================  =========
