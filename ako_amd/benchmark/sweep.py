@@ -9,7 +9,7 @@ output rows follow the reference's ``comparisons[]`` format (what
 ``ako/benchmark/rmsnorm_bench.py`` and ``rope_bench.py`` wrote), one report
 per operation, plus a summary with the HIP win rate.
 
-    python -m ako_amd.benchmark.sweep --out gpurun_out/selection [--ops rmsnorm,rope]
+    python -m ako_amd.benchmark.sweep --out out/selection [--ops rmsnorm,rope]
 """
 
 from __future__ import annotations

@@ -8,7 +8,7 @@ reported. ``compare_bench_lines`` does the same for two ``bench.py`` JSON
 lines: the step throughput, every per-kernel and extra cell's bandwidth (or
 graph-replay time for decode-size cells) and the decoder timings.
 
-    python -m ako_amd.validation.regression CURRENT.json BASELINE.json [--rtol 0.1]
+    python -m ako_amd.validation.regression CURRENT.json PREVIOUS.json [--rtol 0.1]
 """
 
 from __future__ import annotations
