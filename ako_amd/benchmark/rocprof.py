@@ -100,6 +100,41 @@ def traffic(fetch_csv: Path, write_csv: Path, manifest_path: Path) -> dict[str, 
     }
 
 
+def counters_by_cell(path: Path, manifest_path: Path) -> dict[str, dict[str, float]]:
+    """Mean per dispatch of every counter in a ``--pmc`` collection, per cell of
+    the launch manifest (instances of a counter summed within a dispatch)."""
+    manifest = json.loads(Path(manifest_path).read_text())
+    per_dispatch: dict[int, dict[str, float]] = {}
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            d = per_dispatch.setdefault(int(r["Dispatch_Id"]), {})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    order = manifest["dispatches"]
+    ids = sorted(per_dispatch)[-len(order):]
+    if len(ids) != len(order):
+        raise ValueError(f"{len(per_dispatch)} dispatches recorded, manifest lists {len(order)}")
+    sums: dict[str, dict[str, float]] = {}
+    counts: dict[str, int] = {}
+    for spec, did in zip(order, ids):
+        cell = spec["cell"]
+        acc = sums.setdefault(cell, {})
+        for name, value in per_dispatch[did].items():
+            acc[name] = acc.get(name, 0.0) + value
+        counts[cell] = counts.get(cell, 0) + 1
+    return {cell: {k: v / counts[cell] for k, v in acc.items()} for cell, acc in sums.items()}
+
+
+def counters_markdown(cells: dict[str, dict[str, float]], command: str, title: str, note: str = "") -> str:
+    names = sorted({n for c in cells.values() for n in c})
+    lines = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
+    if note:
+        lines += [note, ""]
+    lines += ["| cell | " + " | ".join(names) + " |", "|---|" + "---:|" * len(names)]
+    for cell, vals in cells.items():
+        lines.append(f"| {cell} | " + " | ".join(f"{vals.get(n, 0.0):.4g}" for n in names) + " |")
+    return "\n".join(lines) + "\n"
+
+
 def read_kernel_trace(path: Path) -> list[tuple[str, int, int]]:
     """``(kernel name, start ns, end ns)`` rows of a ``*_kernel_trace.csv``, by start."""
     with open(path, newline="") as fh:
@@ -202,6 +237,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--manifest", type=Path)
     ap.add_argument("--stats", type=Path, help="a *_kernel_stats.csv to summarise instead")
     ap.add_argument("--trace", type=Path, help="a *_kernel_trace.csv: per-step breakdown of its tail")
+    ap.add_argument("--pmc", type=Path, help="a *_counter_collection.csv: every counter per cell (with --manifest)")
+    ap.add_argument("--note", default="", help="with --pmc: a sentence placed above the table")
     ap.add_argument("--tail-ms", type=float, default=None, help="with --trace: window at the end of the run")
     ap.add_argument("--steps", type=int, default=None, help="with --trace: steps inside the window")
     ap.add_argument("--marker", default=None, help="with --trace: a kernel launched once per step")
@@ -210,11 +247,15 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--md", type=Path, required=True)
     ap.add_argument("--json", type=Path, help="also write the figures as JSON (e.g. next to a BenchmarkReport)")
     args = ap.parse_args(argv)
-    if args.trace:
+    if args.pmc:
+        cells = counters_by_cell(args.pmc, args.manifest)
+        args.md.write_text(counters_markdown(cells, args.command, args.title, args.note))
+        record: dict[str, Any] = {"kind": "counters_by_cell", "title": args.title, "cells": cells}
+    elif args.trace:
         result = tail_breakdown(read_kernel_trace(args.trace), args.steps, tail_ms=args.tail_ms,
                                 marker=args.marker)
         args.md.write_text(breakdown_markdown(result, args.command, args.title))
-        record: dict[str, Any] = {"kind": "trace_tail_breakdown", "title": args.title, **result}
+        record = {"kind": "trace_tail_breakdown", "title": args.title, **result}
     elif args.stats:
         rows = read_kernel_stats(args.stats)
         args.md.write_text(stats_markdown(rows, args.command, args.title))

@@ -93,3 +93,21 @@ def test_kernel_stats_and_trace_tail(tmp_path) -> None:
     assert {k["name"]: k["calls_per_step"] for k in marked["kernels"]} == {"gemv": 1.0, "norm": 1.0}
     with pytest.raises(ValueError, match="need"):
         rocprof.tail_breakdown(rows, 9, marker="norm")
+
+
+def test_counters_by_cell_averages_each_cell(tmp_path) -> None:
+    manifest = {"dispatches": [{"cell": "a", "alg_bytes": 1}, {"cell": "a", "alg_bytes": 1},
+                               {"cell": "b", "alg_bytes": 1}]}
+    (tmp_path / "m.json").write_text(json.dumps(manifest))
+    path = tmp_path / "c.csv"
+    with open(path, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=COUNTER_FIELDS)
+        w.writeheader()
+        w.writerow({"Dispatch_Id": 0, "Kernel_Name": "setup", "Counter_Name": "X", "Counter_Value": 99})
+        for did, (x, y) in enumerate([(1, 10), (3, 30), (5, 50)], start=1):
+            for part in (x / 2, x / 2):  # two instances per dispatch
+                w.writerow({"Dispatch_Id": did, "Kernel_Name": "k", "Counter_Name": "X", "Counter_Value": part})
+            w.writerow({"Dispatch_Id": did, "Kernel_Name": "k", "Counter_Name": "Y", "Counter_Value": y})
+    cells = rocprof.counters_by_cell(path, tmp_path / "m.json")
+    assert cells == {"a": {"X": 2.0, "Y": 20.0}, "b": {"X": 5.0, "Y": 50.0}}
+    assert "| a | 2 | 20 |" in rocprof.counters_markdown(cells, "cmd", "t")
