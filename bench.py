@@ -108,7 +108,10 @@ def main() -> int:
     ms_per_step = total_ms / args.steps
     value = bytes_per_step * args.steps / (total_ms * 1e-3) / 1e9
     log(f"timed: {ms_per_step:.3f} ms/step, {value:.1f} GB/s ({100 * value / peak:.1f}% of {peak:.0f})")
-    per_launch = rf.time_each_launch(calls, steps=max(3, min(args.steps, 10)))
+    # The dominant kernel's launch duration: the same K steps again, now with an
+    # event pair around every launch (kept out of the region above so that the
+    # step time holds nothing but the kernels and their launches).
+    per_launch = rf.time_each_launch(calls, steps=args.steps)
     dominant = max(per_launch, key=lambda s: s.mean_ms)
     per_kernel = [s.to_dict(peak) for s in per_launch]
 
@@ -122,6 +125,8 @@ def main() -> int:
         "traffic": None,
         "alg_bytes_per_launch": dominant.alg_bytes,
         "mean_launch_us": round(dominant.mean_ms * 1e3, 2),
+        "launches_timed": len(dominant.durations_ms),
+        "timing": "HIP events around each launch on the launch stream, over the same K steps as value",
     }
     if args.traffic.exists():
         from ako_amd.benchmark.rocprof import load_traffic_md
