@@ -221,3 +221,23 @@ def test_torch_binding_matches_the_ctypes_path() -> None:
         y_side = fast.rmsnorm(x, w, 1e-6)
     torch.cuda.current_stream().wait_stream(side)
     assert torch.equal(y_side, rm.rmsnorm_hip_ctypes(x, w, 1e-6))
+
+
+@pytest.mark.parametrize("n_kv_heads", [4, 2])
+def test_stack_on_hip_kernels_matches_hugging_face_llama(n_kv_heads: int) -> None:
+    """The decoder with the HIP kernels (fp32) against Hugging Face's LlamaModel
+    carrying the same weights, prompt and cached decoding, on the GPU."""
+    from tests.test_model import _hf_pair
+
+    hf, stacks = _hf_pair(n_kv_heads)
+    hf, stack = hf.to(DEV), stacks["ako"].to(DEV)
+    ids = torch.randint(0, 50, (1, 12), generator=torch.Generator().manual_seed(2)).to(DEV)
+    with torch.no_grad():
+        want = hf(input_ids=ids).last_hidden_state
+        emb = hf.embed_tokens(ids)
+        torch.testing.assert_close(stack(emb), want, atol=2e-5, rtol=2e-5)
+        for cache in (stack.new_kv_cache(16), stack.new_static_cache(16)):
+            got = [stack(emb[:, :9], kv_cache=cache)[:, -1]]
+            for t in range(9, 12):
+                got.append(stack(emb[:, t:t + 1], kv_cache=cache)[:, -1])
+            torch.testing.assert_close(torch.stack(got, 1), want[:, 8:12], atol=2e-5, rtol=2e-5)

@@ -92,3 +92,55 @@ def test_static_cache_decode_matches_cat_cache() -> None:
     assert int(static.pos) == 12 and static.length == 7
     with pytest.raises(ValueError, match="overflow"):
         static.update(0, torch.zeros(1, 20, 2, 16), torch.zeros(1, 20, 2, 16))
+
+
+def _hf_pair(n_kv_heads: int):
+    """A small Hugging Face LlamaModel (random weights, built offline from a
+    config) and this package's stack carrying the same weights."""
+    transformers = pytest.importorskip("transformers")
+    from ako_amd.models.decoder import DecoderStack
+
+    hf_cfg = transformers.LlamaConfig(hidden_size=64, num_hidden_layers=2, num_attention_heads=4,
+                                      num_key_value_heads=n_kv_heads, intermediate_size=96, vocab_size=50,
+                                      max_position_embeddings=64, rms_norm_eps=1e-6, rope_theta=10000.0)
+    hf_cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    hf = transformers.LlamaModel(hf_cfg).eval().to(torch.float32)
+    with torch.no_grad():
+        for p in hf.parameters():
+            p.normal_(0.0, 0.05)
+    cfg = ModelConfig(hidden_dim=64, n_layers=2, n_heads=4, n_kv_heads=n_kv_heads, intermediate_dim=96,
+                      max_seq_len=64, vocab_size=50, eps=1e-6, rope_base=10000.0)
+    stacks = {}
+    for backend in ("torch", "ako"):
+        stack = DecoderStack(cfg, backend).eval()
+        with torch.no_grad():
+            for ours, theirs in zip(stack.layers, hf.layers):
+                for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+                    getattr(ours.attention, name).weight.copy_(getattr(theirs.self_attn, name).weight)
+                for name in ("gate_proj", "up_proj", "down_proj"):
+                    getattr(ours.mlp, name).weight.copy_(getattr(theirs.mlp, name).weight)
+                ours.input_norm_weight.copy_(theirs.input_layernorm.weight)
+                ours.post_attention_norm_weight.copy_(theirs.post_attention_layernorm.weight)
+            stack.final_norm_weight.copy_(hf.norm.weight)
+        stacks[backend] = stack
+    return hf, stacks
+
+
+@pytest.mark.parametrize("n_kv_heads", [4, 2])
+def test_stack_matches_hugging_face_llama(n_kv_heads: int) -> None:
+    """An independent implementation of the same architecture (the reference's
+    tests/test_hf_loader.py compares against it too): hidden states of a
+    prompt, and token-by-token decoding through the KV caches, within 1e-5."""
+    hf, stacks = _hf_pair(n_kv_heads)
+    ids = torch.randint(0, 50, (1, 12), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        want = hf(input_ids=ids).last_hidden_state
+        emb = hf.embed_tokens(ids)
+        for backend, stack in stacks.items():
+            assert_close(stack(emb), want, atol=1e-5, rtol=1e-5)
+            for cache in (stack.new_kv_cache(), stack.new_kv_cache(16), stack.new_static_cache(16)):
+                got = [stack(emb[:, :9], kv_cache=cache)[:, -1]]
+                for t in range(9, 12):
+                    got.append(stack(emb[:, t:t + 1], kv_cache=cache)[:, -1])
+                assert_close(torch.stack(got, 1), want[:, 8:12], atol=1e-5, rtol=1e-5)
