@@ -61,9 +61,10 @@ def log(msg: str) -> None:
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the kernels shard "
-              "with no communication, so the N-GPU figure is N x the one-GPU figure by construction "
-              "and is not measured here.", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported. Split by rows or "
+              "tokens (data or sequence parallelism) the kernels need no communication, so the N-GPU "
+              "figure is N x the one-GPU figure by construction; it is not measured here.",
+              file=sys.stderr)
         return 2
 
     import torch
