@@ -149,7 +149,21 @@ def build_torch_binding(*, verbose: bool = False) -> Path:
     return out
 
 
+COPY_PROBE_SOURCE = PACKAGE_DIR / "benchmark" / "copy_ceiling.hip"
+COPY_PROBE_PATH = LIB_DIR / "copy_ceiling"
+
+
+def build_copy_probe(*, verbose: bool = False) -> Path:
+    """Compile the stand-alone copy-ceiling program (size-dependent HBM ceiling)."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = COPY_PROBE_PATH.with_name(COPY_PROBE_PATH.name + f".tmp{os.getpid()}")
+    _run([_hipcc(), *compile_flags(), str(COPY_PROBE_SOURCE), "-o", str(tmp)], verbose)
+    os.replace(tmp, COPY_PROBE_PATH)
+    return COPY_PROBE_PATH
+
+
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
     print(build_torch_binding(verbose="-v" in sys.argv))
+    print(build_copy_probe(verbose="-v" in sys.argv))

@@ -1,0 +1,104 @@
+// Size-dependent streaming ceiling of one GPU: the per-launch time of a plain
+// device copy (16-byte packets, one per lane, non-temporal loads and stores)
+// at given byte counts, with cold buffers.
+//
+// A streaming kernel that reads and writes B bytes cannot be expected to beat
+// a copy that moves the same B bytes, so the copy's fraction of the HBM peak at
+// that size is the practical roofline of each hot-path cell. It falls with
+// size because every launch pays a roughly fixed ramp-up and drain.
+//
+// Usage: copy_ceiling [bytes_per_buffer ...]   (default: the hot-path cell sizes)
+// Prints one JSON object per size and block shape:
+//   {"bytes_per_buffer": N, "traffic_bytes": 2N, "block": 256, "us": t,
+//    "gbps": 2N/t, "frac": gbps/8000}
+// Buffers rotate through a 2 GiB source pool and a 2 GiB destination pool, so
+// consecutive launches never find their data in the 256 MB MALL or the L2s.
+// Each launch is bracketed by its own events; the median of 22 launches (after
+// 3 warm-up launches) is reported.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+#define CHECK(x)                                                                         \
+  do {                                                                                   \
+    hipError_t err_ = (x);                                                               \
+    if (err_ != hipSuccess) {                                                            \
+      std::fprintf(stderr, "copy_ceiling: %s at line %d\n", hipGetErrorString(err_), __LINE__); \
+      std::exit(1);                                                                      \
+    }                                                                                    \
+  } while (0)
+
+template <int BLOCK>
+__global__ __launch_bounds__(BLOCK) void copy_packets(const u32x4* __restrict__ a, u32x4* __restrict__ b, long n) {
+  const long i = (long)blockIdx.x * BLOCK + threadIdx.x;
+  if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(a + i), b + i);
+}
+
+static constexpr long kPool = 1L << 31;
+static constexpr double kPeakGBs = 8000.0;
+
+int main(int argc, char** argv) {
+  std::vector<long> sizes;
+  for (int i = 1; i < argc; ++i) sizes.push_back(std::atol(argv[i]));
+  if (sizes.empty()) {
+    // Half the algorithmic bytes of each prefill cell (a copy of N bytes moves 2N):
+    // RoPE (4, 2048, h, 128) half precision, k (h = 8), q (h = 32) and q + k in one
+    // launch; RMSNorm, 16384 rows of 4096 / 8192 / 16384 half elements (the
+    // residual variant moves twice the plain one); SwiGLU bf16 M x 14336 at
+    // M = 4096 and 16384 (three streams, so only roughly a copy).
+    sizes = {17039360L, 67371008L, 84148224L, 128L << 20, 176160768L, 256L << 20, 512L << 20, 704643072L, 1L << 30};
+  }
+  for (long bytes : sizes) {
+    if (bytes < 16 || bytes > kPool || bytes % 16 != 0) {
+      std::fprintf(stderr, "copy_ceiling: size %ld must be a multiple of 16 in [16, %ld]\n", bytes, kPool);
+      return 2;
+    }
+  }
+  char* src = nullptr;
+  char* dst = nullptr;
+  CHECK(hipMalloc(&src, kPool));
+  CHECK(hipMalloc(&dst, kPool));
+  CHECK(hipMemset(src, 1, kPool));
+  CHECK(hipMemset(dst, 0, kPool));
+  hipEvent_t start, stop;
+  CHECK(hipEventCreate(&start));
+  CHECK(hipEventCreate(&stop));
+  for (long bytes : sizes) {
+    const long n = bytes / 16;
+    const long slots = kPool / bytes;  // >= 1; slot s spans [s*bytes, (s+1)*bytes) of each pool
+    for (int block : {256, 1024}) {
+      std::vector<float> ms_list;
+      for (int rep = 0; rep < 25; ++rep) {
+        const long off = (rep % slots) * bytes;
+        const u32x4* a = reinterpret_cast<const u32x4*>(src + off);
+        u32x4* b = reinterpret_cast<u32x4*>(dst + off);
+        CHECK(hipEventRecord(start));
+        if (block == 256)
+          hipLaunchKernelGGL(copy_packets<256>, dim3((n + 255) / 256), dim3(256), 0, 0, a, b, n);
+        else
+          hipLaunchKernelGGL(copy_packets<1024>, dim3((n + 1023) / 1024), dim3(1024), 0, 0, a, b, n);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(stop));
+        CHECK(hipEventSynchronize(stop));
+        float ms = 0.f;
+        CHECK(hipEventElapsedTime(&ms, start, stop));
+        if (rep >= 3) ms_list.push_back(ms);
+      }
+      std::sort(ms_list.begin(), ms_list.end());
+      const double us = 1e3 * ms_list[ms_list.size() / 2];
+      const double gbps = 2.0 * bytes / (us * 1e-6) / 1e9;
+      std::printf("{\"bytes_per_buffer\": %ld, \"traffic_bytes\": %ld, \"block\": %d, \"us\": %.2f, "
+                  "\"gbps\": %.1f, \"frac\": %.4f}\n",
+                  bytes, 2 * bytes, block, us, gbps, gbps / kPeakGBs);
+      std::fflush(stdout);
+    }
+  }
+  CHECK(hipFree(src));
+  CHECK(hipFree(dst));
+  return 0;
+}

@@ -1,6 +1,8 @@
 """Reading rocprofv3 output: kernel statistics and HBM traffic counters.
 
 ``read_kernel_stats`` parses ``--stats`` output (``*_kernel_stats.csv``).
+``durations_by_grid`` groups a ``--kernel-trace`` (``*_kernel_trace.csv``) by
+launch shape, so cells that share a kernel are timed apart.
 ``traffic`` combines two counter passes (``--pmc FETCH_SIZE`` and ``--pmc
 WRITE_SIZE``, each a separate run: one pass cannot hold both) over the launch
 sequence of ``ako_amd.benchmark.counters``. Both counters report KiB per
@@ -143,6 +145,41 @@ def read_kernel_trace(path: Path) -> list[tuple[str, int, int]]:
     return sorted(rows, key=lambda r: r[1])
 
 
+def durations_by_grid(path: Path, skip: int = 0) -> list[dict[str, Any]]:
+    """Kernel durations of a ``*_kernel_trace.csv`` grouped by (kernel, workgroup
+    size, grid size): one group per launch shape, so the cells of a benchmark
+    that share a kernel but not a shape come apart. ``skip`` drops each group's
+    first launches (warm-up)."""
+    groups: dict[tuple[str, int, int], list[int]] = {}
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            key = (r["Kernel_Name"], int(r["Workgroup_Size_X"]), int(r["Grid_Size_X"]))
+            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    out = []
+    for (name, wg, grid), ns in groups.items():
+        ns = ns[skip:] if len(ns) > skip else ns
+        out.append({"name": name, "workgroup": wg, "grid": grid, "calls": len(ns),
+                    "median_us": statistics.median(ns) / 1e3, "mean_us": statistics.fmean(ns) / 1e3,
+                    "min_us": min(ns) / 1e3})
+    return sorted(out, key=lambda g: (g["name"], g["grid"], g["workgroup"]))
+
+
+def grid_markdown(groups: list[dict[str, Any]], command: str, title: str, note: str = "",
+                  name_filter: str | None = None) -> str:
+    lines = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
+    if note:
+        lines += [note, ""]
+    lines += ["| kernel | workgroup | grid (work-items) | calls | median us | mean us | min us |",
+              "|---|---:|---:|---:|---:|---:|---:|"]
+    for g in groups:
+        if name_filter and name_filter not in g["name"]:
+            continue
+        name = g["name"] if len(g["name"]) <= 90 else g["name"][:87] + "..."
+        lines.append(f"| `{name}` | {g['workgroup']} | {g['grid']} | {g['calls']} | {g['median_us']:.2f} | "
+                     f"{g['mean_us']:.2f} | {g['min_us']:.2f} |")
+    return "\n".join(lines) + "\n"
+
+
 def tail_breakdown(rows: list[tuple[str, int, int]], steps: int, *, tail_ms: float | None = None,
                    marker: str | None = None) -> dict[str, Any]:
     """Kernel time per step over the last ``steps`` steps of a trace (e.g. the
@@ -238,7 +275,11 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--stats", type=Path, help="a *_kernel_stats.csv to summarise instead")
     ap.add_argument("--trace", type=Path, help="a *_kernel_trace.csv: per-step breakdown of its tail")
     ap.add_argument("--pmc", type=Path, help="a *_counter_collection.csv: every counter per cell (with --manifest)")
-    ap.add_argument("--note", default="", help="with --pmc: a sentence placed above the table")
+    ap.add_argument("--note", default="", help="with --pmc or --by-grid: a sentence placed above the table")
+    ap.add_argument("--by-grid", action="store_true",
+                    help="with --trace: durations per (kernel, workgroup, grid) instead of a tail breakdown")
+    ap.add_argument("--skip", type=int, default=0, help="with --by-grid: warm-up launches dropped per group")
+    ap.add_argument("--filter", default=None, help="with --by-grid: only kernels whose name contains this")
     ap.add_argument("--tail-ms", type=float, default=None, help="with --trace: window at the end of the run")
     ap.add_argument("--steps", type=int, default=None, help="with --trace: steps inside the window")
     ap.add_argument("--marker", default=None, help="with --trace: a kernel launched once per step")
@@ -251,6 +292,12 @@ def main(argv: list[str] | None = None) -> int:
         cells = counters_by_cell(args.pmc, args.manifest)
         args.md.write_text(counters_markdown(cells, args.command, args.title, args.note))
         record: dict[str, Any] = {"kind": "counters_by_cell", "title": args.title, "cells": cells}
+    elif args.trace and args.by_grid:
+        groups = durations_by_grid(args.trace, args.skip)
+        if args.filter:
+            groups = [g for g in groups if args.filter in g["name"]]
+        args.md.write_text(grid_markdown(groups, args.command, args.title, args.note))
+        record = {"kind": "durations_by_grid", "title": args.title, "groups": groups}
     elif args.trace:
         result = tail_breakdown(read_kernel_trace(args.trace), args.steps, tail_ms=args.tail_ms,
                                 marker=args.marker)

@@ -111,3 +111,31 @@ def test_counters_by_cell_averages_each_cell(tmp_path) -> None:
     cells = rocprof.counters_by_cell(path, tmp_path / "m.json")
     assert cells == {"a": {"X": 2.0, "Y": 20.0}, "b": {"X": 5.0, "Y": 50.0}}
     assert "| a | 2 | 20 |" in rocprof.counters_markdown(cells, "cmd", "t")
+
+
+def test_durations_by_grid_separate_launch_shapes(tmp_path) -> None:
+    """One kernel launched at two grid sizes is two groups; warm-up launches drop per group."""
+    trace = tmp_path / "t.csv"
+    fields = ["Kernel_Name", "Workgroup_Size_X", "Grid_Size_X", "Start_Timestamp", "End_Timestamp"]
+    with open(trace, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=fields)
+        w.writeheader()
+        t = 0
+        for dur_ns in (50_000, 10_000, 10_000, 12_000):  # the first is a slow warm-up
+            w.writerow({"Kernel_Name": "rope", "Workgroup_Size_X": 256, "Grid_Size_X": 4096,
+                        "Start_Timestamp": t, "End_Timestamp": t + dur_ns})
+            t += 100_000
+        for dur_ns in (90_000, 30_000, 40_000):
+            w.writerow({"Kernel_Name": "rope", "Workgroup_Size_X": 256, "Grid_Size_X": 16384,
+                        "Start_Timestamp": t, "End_Timestamp": t + dur_ns})
+            t += 100_000
+    groups = rocprof.durations_by_grid(trace, skip=1)
+    assert [(g["grid"], g["calls"]) for g in groups] == [(4096, 3), (16384, 2)]
+    assert groups[0]["median_us"] == pytest.approx(10.0) and groups[0]["min_us"] == pytest.approx(10.0)
+    assert groups[1]["mean_us"] == pytest.approx(35.0)
+    md = rocprof.grid_markdown(groups, "cmd", "t")
+    assert "| `rope` | 256 | 16384 | 2 | 35.00 | 35.00 | 30.00 |" in md
+    out = tmp_path / "g.md"
+    assert rocprof.main(["--trace", str(trace), "--by-grid", "--skip", "1", "--md", str(out),
+                         "--json", str(tmp_path / "g.json")]) == 0
+    assert json.loads((tmp_path / "g.json").read_text())["kind"] == "durations_by_grid"
