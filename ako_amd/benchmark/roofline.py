@@ -208,3 +208,44 @@ def time_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int) -> flo
     end.record(stream)
     torch.cuda.synchronize()
     return begin.elapsed_time(end) / launches
+
+
+def parse_copy_ceiling(text: str) -> dict[str, Any] | None:
+    """The fastest block shape among the JSON lines printed by ``copy_ceiling``
+    for one size (None when there are none)."""
+    import json
+
+    rows = []
+    for line in text.splitlines():
+        line = line.strip()
+        if line.startswith("{"):
+            rows.append(json.loads(line))
+    if not rows:
+        return None
+    return max(rows, key=lambda r: r["gbps"])
+
+
+def copy_same_bytes(alg_bytes: int, *, timeout_s: float = 120.0) -> dict[str, Any] | None:
+    """Time a plain device copy that moves about ``alg_bytes`` (half read, half
+    written) with ``ako_amd/_lib/copy_ceiling``, run as a child process.
+
+    It is the practical ceiling for a streaming kernel of that size: launches
+    pay a roughly fixed ramp-up, so the copy's share of the HBM peak falls with
+    the byte count. Returns the probe's record for its fastest block shape, or
+    None when the probe is not built or fails (it is a reference figure, not
+    part of any result)."""
+    import subprocess
+
+    from ako_amd._build import COPY_PROBE_PATH
+
+    per_buffer = (int(alg_bytes) // 2) // 16 * 16
+    if per_buffer < 16 or not COPY_PROBE_PATH.exists():
+        return None
+    try:
+        proc = subprocess.run([str(COPY_PROBE_PATH), str(per_buffer)], capture_output=True, text=True,
+                              timeout=timeout_s)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    if proc.returncode != 0:
+        return None
+    return parse_copy_ceiling(proc.stdout)

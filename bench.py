@@ -11,7 +11,9 @@ step x steps / elapsed device time, in GB/s.
 
 Also reported on the same line:
   roofline      the dominant kernel (largest share of the step) with its
-                per-launch duration from HIP events on the launch stream;
+                per-launch duration from HIP events on the launch stream,
+                and a plain device copy of the same byte count timed the same
+                way (copy_same_bytes: the size's practical ceiling);
   per_kernel    every launch of the step, the RoPE and SwiGLU
                 (configs[3]) prefill cells and the decode-size cells;
   decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
@@ -139,6 +141,18 @@ def main() -> int:
         for row in per_kernel:
             if row["name"] in measured:
                 row["traffic_bytes"] = measured[row["name"]]
+    copy = rf.copy_same_bytes(dominant.alg_bytes)
+    if copy is not None:
+        roofline["copy_same_bytes"] = {
+            "gbps": copy["gbps"],
+            "frac": copy["frac"],
+            "kernel_over_copy": round(dominant.gbps() / copy["gbps"], 4),
+            "source": f"ako_amd/_lib/copy_ceiling {copy['bytes_per_buffer']} (plain 16-byte-packet copy "
+                      f"moving {copy['traffic_bytes']} bytes, cold buffers, per-launch events, "
+                      f"{copy['block']}-lane workgroups)",
+        }
+        log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
+            f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")
     del calls
     torch.cuda.empty_cache()
 

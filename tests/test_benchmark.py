@@ -178,3 +178,17 @@ def test_env_samples_degrade_to_none() -> None:
     assert set(sample) == {"sm_clock_mhz", "temp_c", "power_w", "throttle_reasons"}
     assert all(v is None for v in sample.values())
     assert host_cpu()["os_cpu_count"] >= 1
+
+
+def test_copy_ceiling_lines_pick_the_fastest_shape(monkeypatch, tmp_path) -> None:
+    text = ("noise\n"
+            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 256, "us": 2.0, "gbps": 0.064, "frac": 0.1}\n'
+            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 1024, "us": 1.0, "gbps": 0.128, "frac": 0.2}\n')
+    best = rf.parse_copy_ceiling(text)
+    assert best["block"] == 1024 and best["frac"] == 0.2
+    assert rf.parse_copy_ceiling("no json here") is None
+    # Without the built probe the figure is simply absent.
+    import ako_amd._build as build
+
+    monkeypatch.setattr(build, "COPY_PROBE_PATH", tmp_path / "missing")
+    assert rf.copy_same_bytes(1 << 20) is None
