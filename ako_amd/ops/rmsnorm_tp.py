@@ -12,9 +12,10 @@ squares needs every slice. The rank-local work splits in two:
 3. ``rmsnorm_shard_apply``: ``y = (s * rsqrt(total / hidden + eps)) * w`` on
    the slice, with ``hidden`` the full row length.
 
-This build runs on one GPU and contains no collective: ``rmsnorm_sharded``
-runs every slice of a row on the one device and sums the partials with
-``torch.sum`` where a multi-GPU caller would all-reduce them. That shows the
+``rmsnorm_tp`` is one rank's part in a ``torch.distributed`` group: partial,
+all-reduce, apply. ``rmsnorm_sharded`` runs every slice of a row on one
+device and sums the partials with ``torch.sum`` where the ranks would
+all-reduce them. That shows the
 per-rank kernels at their real shapes and that the slices compose to the
 full-row result. The HIP halves are ``ako_rmsnorm_shard_partial_fwd`` and
 ``ako_rmsnorm_shard_apply_fwd``; the ``*_ref`` functions are the same
@@ -128,8 +129,43 @@ def rmsnorm_sharded(
     return torch.cat(ys, -1), torch.cat([s for s, _ in parts], -1)
 
 
+def rmsnorm_tp(
+    x: torch.Tensor,
+    residual: torch.Tensor | None,
+    weight: torch.Tensor,
+    hidden: int,
+    eps: float = 1e-6,
+    *,
+    group=None,
+    partial_fn: Callable = rmsnorm_shard_partial_hip,
+    apply_fn: Callable = rmsnorm_shard_apply_hip,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """This rank's slice of ``(rmsnorm(x + residual), x + residual)`` in a
+    ``torch.distributed`` group whose ranks hold the column slices of every row.
+
+    ``x``, ``residual`` and ``weight`` are the rank's slices; ``hidden`` is the
+    full row length. The per-row partial sums of squares (one fp32 per row) are
+    summed over the group with one all-reduce. Over RCCL (backend ``"nccl"``)
+    the device tensor is reduced in place; gloo gets a host copy, made and
+    copied back synchronously, since gloo is given CPU tensors only.
+    """
+    import torch.distributed as dist
+
+    if weight.shape[-1] != x.shape[-1]:
+        raise ValueError(f"weight slice {tuple(weight.shape)} does not match x slice {tuple(x.shape)}")
+    s, partial = partial_fn(x, residual)
+    if partial.is_cuda and dist.get_backend(group) == "gloo":
+        host = partial.cpu()
+        dist.all_reduce(host, op=dist.ReduceOp.SUM, group=group)
+        partial.copy_(host)
+    else:
+        dist.all_reduce(partial, op=dist.ReduceOp.SUM, group=group)
+    return apply_fn(s, weight, partial, hidden, eps), s
+
+
 __all__ = [
     "rmsnorm_sharded",
+    "rmsnorm_tp",
     "rmsnorm_shard_apply_hip",
     "rmsnorm_shard_apply_ref",
     "rmsnorm_shard_partial_hip",

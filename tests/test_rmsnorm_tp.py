@@ -117,3 +117,59 @@ def test_hip_partial_sums_and_weights() -> None:
     assert rep["passed"] and rep["err_ulps"] <= MAX_ULPS, rep
     with pytest.raises(ValueError, match="float32"):
         rmsnorm_shard_apply_hip(s, w32, part.double(), 2048)
+
+
+def _free_port() -> int:
+    import socket
+
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        return s.getsockname()[1]
+
+
+def _run_ranks(tmp_path, world: int, device: str, dtype: torch.dtype, rows: int, hidden: int,
+               use_hip: bool) -> None:
+    """Spawn ``world`` ranks over gloo; check the concatenated slices against
+    the full-row reference (bit-equal residual sum, normalised rows within the
+    gate and 2 ulps of the oracle)."""
+    import torch.multiprocessing as mp
+
+    from tests._tp_worker import full_inputs, rank_main
+
+    mp.spawn(rank_main, args=(world, _free_port(), str(tmp_path), device, str(dtype).split(".")[-1], rows,
+                              hidden, use_hip), nprocs=world, join=True)
+    parts = [torch.load(tmp_path / f"rank{i}.pt", weights_only=True) for i in range(world)]
+    y = torch.cat([p["y"] for p in parts], -1)
+    s = torch.cat([p["s"] for p in parts], -1)
+    yp = torch.cat([p["y_plain"] for p in parts], -1)
+    x, r, w = full_inputs(rows, hidden, dtype)
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), 1e-6, dtype=NAMES[dtype])
+    np.testing.assert_array_equal(to_np(s), es)
+    rep = oracle.gate(ey, to_np(y), NAMES[dtype])
+    assert rep["passed"] and rep["err_ulps"] <= MAX_ULPS, rep
+    rep = oracle.gate(oracle.rmsnorm(to_np(x), to_np(w), 1e-6, dtype=NAMES[dtype]), to_np(yp), NAMES[dtype])
+    assert rep["passed"] and rep["err_ulps"] <= MAX_ULPS, rep
+
+
+def test_two_gloo_ranks_compose_to_the_full_row(tmp_path) -> None:
+    """Two processes, each holding half of every row, all-reduce their partial
+    sums over gloo (the PyTorch halves on the CPU)."""
+    _run_ranks(tmp_path, 2, "cpu", torch.bfloat16, 16, 1024, use_hip=False)
+
+
+def test_rank_rejects_a_mismatched_weight_slice() -> None:
+    from ako_amd.ops.rmsnorm_tp import rmsnorm_tp
+
+    x = torch.zeros(2, 8)
+    with pytest.raises(ValueError, match="weight slice"):
+        rmsnorm_tp(x, None, torch.ones(16), 16, partial_fn=rmsnorm_shard_partial_ref,
+                   apply_fn=rmsnorm_shard_apply_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_two_ranks_on_the_gpu_compose_to_the_full_row(tmp_path, dtype) -> None:
+    """The HIP halves in two processes sharing cuda:0; the partial sums cross
+    gloo through host copies (4096 rows x 8192, each rank a 4096-wide slice)."""
+    _run_ranks(tmp_path, 2, "cuda:0", dtype, 4096, 8192, use_hip=True)
