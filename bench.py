@@ -149,7 +149,7 @@ def main() -> int:
             "kernel_over_copy": round(dominant.gbps() / copy["gbps"], 4),
             "source": f"ako_amd/_lib/copy_ceiling {copy['bytes_per_buffer']} (plain 16-byte-packet copy "
                       f"moving {copy['traffic_bytes']} bytes, cold buffers, per-launch events, "
-                      f"{copy['block']}-lane workgroups)",
+                      f"{copy['block']}-lane workgroups, {copy.get('store', 'nt')} stores; the fastest copy found)",
         }
         log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
             f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")
