@@ -116,11 +116,22 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
     if (h < total) {
       const bool first = h < a.t0.heads;
       const bool third = CACHE && h >= h01;
-      const RopeTensorDev& tt = first ? a.t0 : (third ? a.t2 : a.t1);
+      // The tensor is chosen field by field, by value: the fields then come
+      // from scalar kernel-argument loads and a per-lane select. Binding a
+      // reference to the per-lane choice makes the compiler fetch the whole
+      // descriptor with vector loads, a memory round trip that every
+      // wavefront waits for before it can issue its first data load.
+      const auto pick = [&](const auto& f0, const auto& f1, const auto& f2) { return first ? f0 : (third ? f2 : f1); };
+      const void* x = pick(a.t0.x, a.t1.x, a.t2.x);
+      void* y = pick(a.t0.y, a.t1.y, a.t2.y);
+      const int64_t sxb = pick(a.t0.sxb, a.t1.sxb, a.t2.sxb), sxs = pick(a.t0.sxs, a.t1.sxs, a.t2.sxs),
+                    sxh = pick(a.t0.sxh, a.t1.sxh, a.t2.sxh);
+      const int64_t syb = pick(a.t0.syb, a.t1.syb, a.t2.syb), sys = pick(a.t0.sys, a.t1.sys, a.t2.sys),
+                    syh = pick(a.t0.syh, a.t1.syh, a.t2.syh);
       const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
       const int64_t srow = (CACHE && !first) ? p : s;
-      const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh + j * E;
-      dst[it] = static_cast<T*>(tt.y) + b * tt.syb + srow * tt.sys + hh * tt.syh + j * E;
+      const T* src = static_cast<const T*>(x) + b * sxb + s * sxs + hh * sxh + j * E;
+      dst[it] = static_cast<T*>(y) + b * syb + srow * sys + hh * syh + j * E;
       if constexpr (CACHE) copy[it] = third;
       lo[it] = load_pack<T, E, true>(src);
       if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
