@@ -325,20 +325,35 @@ __global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_apply(
   const int64_t row = row0 + blockIdx.x;
   const int tid = threadIdx.x;
   const int nvec = shard / E;
-  const float rstd = rsqrtf(total[row] * inv_h + eps);
   const T* sr = s + row * ss_;
   T* yr = y + row * sy;
-  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
-    const P p = load_pack<T, E, true>(sr + vi * E);
-    float wf[E];
-    load_f32<W, E>(w + vi * E, wf);
+  const auto apply = [&](int vi, const P& p, const float (&wf)[E], float rstd) {
     P o;
 #pragma unroll
     for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(p.e[e]) * rstd) * wf[e]);
     store_pack<T, E, true>(yr + vi * E, o);
+  };
+  // Each lane requests its first packet before the row's total is read: the
+  // total is a dependent read of its own (a scalar load), and computing rstd
+  // first would put that round trip in front of every workgroup's data loads.
+  if (tid < nvec) {
+    const P p0 = load_pack<T, E, true>(sr + tid * E);
+    float wf0[E];
+    load_f32<W, E>(w + tid * E, wf0);
+    const float rstd = rsqrtf(total[row] * inv_h + eps);
+    apply(tid, p0, wf0, rstd);
+    for (int vi = tid + kStreamBlock; vi < nvec; vi += kStreamBlock) {
+      const P p = load_pack<T, E, true>(sr + vi * E);
+      float wf[E];
+      load_f32<W, E>(w + vi * E, wf);
+      apply(vi, p, wf, rstd);
+    }
   }
-  for (int j = nvec * E + tid; j < shard; j += kStreamBlock)
-    yr[j] = from_f32<T>((to_f32(sr[j]) * rstd) * to_f32(w[j]));
+  const int tail0 = nvec * E + tid;
+  if (tail0 < shard) {
+    const float rstd = rsqrtf(total[row] * inv_h + eps);
+    for (int j = tail0; j < shard; j += kStreamBlock) yr[j] = from_f32<T>((to_f32(sr[j]) * rstd) * to_f32(w[j]));
+  }
 }
 
 #ifndef AKO_RMS_NT
