@@ -192,11 +192,14 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
     if (CACHE && (p < 0 || p >= a.cache_len)) continue;
     const bool first = h < a.t0.heads;
     const bool third = CACHE && h >= h01;
-    const RopeTensorDev& tt = first ? a.t0 : (third ? a.t2 : a.t1);
+    // Field by field, by value (scalar loads and a select; see rope_vec).
+    const auto pick = [&](const auto& f0, const auto& f1, const auto& f2) { return first ? f0 : (third ? f2 : f1); };
     const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
     const int64_t srow = (CACHE && !first) ? p : s;
-    const T* src = static_cast<const T*>(tt.x) + b * tt.sxb + s * tt.sxs + hh * tt.sxh;
-    T* dst = static_cast<T*>(tt.y) + b * tt.syb + srow * tt.sys + hh * tt.syh;
+    const T* src = static_cast<const T*>(pick(a.t0.x, a.t1.x, a.t2.x)) + b * pick(a.t0.sxb, a.t1.sxb, a.t2.sxb) +
+                   s * pick(a.t0.sxs, a.t1.sxs, a.t2.sxs) + hh * pick(a.t0.sxh, a.t1.sxh, a.t2.sxh);
+    T* dst = static_cast<T*>(pick(a.t0.y, a.t1.y, a.t2.y)) + b * pick(a.t0.syb, a.t1.syb, a.t2.syb) +
+             srow * pick(a.t0.sys, a.t1.sys, a.t2.sys) + hh * pick(a.t0.syh, a.t1.syh, a.t2.syh);
     const int64_t ia = NEOX ? i : 2 * i;
     const int64_t ib = NEOX ? i + half : 2 * i + 1;
     if (third) {
