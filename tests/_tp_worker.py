@@ -21,7 +21,12 @@ def rank_main(rank: int, world: int, port: int, out_dir: str, device: str, dtype
         rmsnorm_tp,
     )
 
-    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank, world_size=world)
+    import datetime
+
+    # A bounded rendezvous and collective timeout: a rank that fails ends the
+    # test instead of leaving the other waiting for gloo's 30-minute default.
+    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank, world_size=world,
+                            timeout=datetime.timedelta(seconds=60))
     try:
         dtype = getattr(torch, dtype_name)
         x, r, w = full_inputs(rows, hidden, dtype)
