@@ -191,3 +191,37 @@ def test_compile_baselines_are_opt_in(monkeypatch) -> None:
 def test_device_info_cpu() -> None:
     info = get_device_info(torch.device("cpu"))
     assert (info.device_type, info.compute_backend, info.cache_key) == ("cpu", "cpu", "cpu_-1")
+
+
+def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
+    """The reset/clear helpers the reference exposes for tests, and
+    ``load_baseline`` for its regression diffs, behave as their names say."""
+    from ako_amd.benchmark.profiler import profile_cuda
+    from ako_amd.dispatcher import hardware
+    from ako_amd.ops import _registry, rmsnorm_torch
+    from ako_amd.validation.regression import load_baseline
+
+    register_all()
+    assert _registry._registered
+    _registry.reset_registration()
+    assert not _registry._registered
+    register_all()
+    assert _registry._registered
+
+    rmsnorm_torch._compiled["probe"] = object()
+    rmsnorm_torch.reset_compiled_cache()
+    assert rmsnorm_torch._compiled == {}
+
+    first = get_device_info("cpu")
+    assert hardware._device_info.cache_info().currsize >= 1
+    hardware.clear_device_cache()
+    assert hardware._device_info.cache_info().currsize == 0
+    assert get_device_info("cpu") == first
+
+    path = tmp_path / "baseline.json"
+    path.write_text(json.dumps({"comparisons": [{"shape": [1, 2], "selected_kernel": "k"}]}))
+    assert load_baseline(path)["comparisons"][0]["selected_kernel"] == "k"
+
+    with profile_cuda() as prof:
+        torch.ones(4).sum()
+    assert any("sum" in e.name for e in prof.events())
