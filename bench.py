@@ -14,8 +14,10 @@ Also reported on the same line:
                 per-launch duration from HIP events on the launch stream,
                 and a plain device copy of the same byte count timed the same
                 way (copy_same_bytes: the size's practical ceiling);
-  per_kernel    every launch of the step, the RoPE and SwiGLU
-                (configs[3]) prefill cells and the decode-size cells;
+  per_kernel    every launch of the step;
+  extras        the RoPE and SwiGLU cells, the
+                decode-size RMSNorm cells, the KV-cache RoPE and the
+                tensor-parallel RMSNorm halves;
   decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
                 128 greedy steps, eager PyTorch vs the dispatcher, each also
                 with decode steps replayed from a HIP graph;
@@ -64,8 +66,8 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported. Split by rows or "
-              "tokens (data or sequence parallelism) the kernels need no communication, so the N-GPU "
-              "figure is N x the one-GPU figure by construction; it is not measured here.",
+              "tokens (data or sequence parallelism), these kernels need no communication, so the "
+              "N-GPU figure would be N times the one-GPU figure; it is not measured here.",
               file=sys.stderr)
         return 2
 
