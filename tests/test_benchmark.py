@@ -192,3 +192,16 @@ def test_copy_ceiling_lines_pick_the_fastest_shape(monkeypatch, tmp_path) -> Non
 
     monkeypatch.setattr(build, "COPY_PROBE_PATH", tmp_path / "missing")
     assert rf.copy_same_bytes(1 << 20) is None
+
+
+def test_bench_refuses_more_than_one_gpu() -> None:
+    """bench.py measures one GPU; asked for more it exits 2 and says why."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    out = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "4"], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 2
+    assert "measures one GPU" in out.stderr and out.stdout == ""
