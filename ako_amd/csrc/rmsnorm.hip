@@ -317,42 +317,54 @@ __global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_partial(
   }
 }
 
-template <typename T, typename W, int E>
+template <typename T, typename W, int E, int R>
 __global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_apply(
     const T* __restrict__ s, const W* __restrict__ w, const float* __restrict__ total,
-    T* __restrict__ y, int64_t row0, int shard, int64_t ss_, int64_t sy, float inv_h, float eps) {
+    T* __restrict__ y, int64_t row0, int64_t rows, int shard, int64_t ss_, int64_t sy, float inv_h, float eps) {
+  // Each workgroup applies R consecutive rows; a lane holds the same columns of
+  // all R, so the weight packet is read once for R rows.
   using P = Pack<T, E>;
-  const int64_t row = row0 + blockIdx.x;
+  const int64_t first = row0 + static_cast<int64_t>(blockIdx.x) * R;
   const int tid = threadIdx.x;
   const int nvec = shard / E;
-  const T* sr = s + row * ss_;
-  T* yr = y + row * sy;
-  const auto apply = [&](int vi, const P& p, const float (&wf)[E], float rstd) {
+  const auto apply = [&](int64_t row, int vi, const P& p, const float (&wf)[E], float rstd) {
     P o;
 #pragma unroll
     for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(p.e[e]) * rstd) * wf[e]);
-    store_pack<T, E, true>(yr + vi * E, o);
+    store_pack<T, E, true>(y + row * sy + vi * E, o);
   };
-  // Each lane requests its first packet before the row's total is read: the
-  // total is a dependent read of its own (a scalar load), and computing rstd
-  // first would put that round trip in front of every workgroup's data loads.
-  if (tid < nvec) {
-    const P p0 = load_pack<T, E, true>(sr + tid * E);
-    float wf0[E];
-    load_f32<W, E>(w + tid * E, wf0);
-    const float rstd = rsqrtf(total[row] * inv_h + eps);
-    apply(tid, p0, wf0, rstd);
-    for (int vi = tid + kStreamBlock; vi < nvec; vi += kStreamBlock) {
-      const P p = load_pack<T, E, true>(sr + vi * E);
-      float wf[E];
-      load_f32<W, E>(w + vi * E, wf);
-      apply(vi, p, wf, rstd);
+  // The data packets are requested before the rows' totals are read: a total
+  // is a dependent read of its own (a scalar load), and computing rstd first
+  // would put that round trip in front of every workgroup's data loads.
+  float rstd[R];
+  bool have_rstd = false;
+  for (int vi = tid; vi < nvec; vi += kStreamBlock) {
+    P p[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+      if (first + k < rows) p[k] = load_pack<T, E, true>(s + (first + k) * ss_ + vi * E);
+    float wf[E];
+    load_f32<W, E>(w + vi * E, wf);
+    if (!have_rstd) {
+#pragma unroll
+      for (int k = 0; k < R; ++k) rstd[k] = first + k < rows ? rsqrtf(total[first + k] * inv_h + eps) : 0.f;
+      have_rstd = true;
     }
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+      if (first + k < rows) apply(first + k, vi, p[k], wf, rstd[k]);
   }
   const int tail0 = nvec * E + tid;
   if (tail0 < shard) {
-    const float rstd = rsqrtf(total[row] * inv_h + eps);
-    for (int j = tail0; j < shard; j += kStreamBlock) yr[j] = from_f32<T>((to_f32(sr[j]) * rstd) * to_f32(w[j]));
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int64_t row = first + k;
+      if (row >= rows) break;
+      const float rs = rsqrtf(total[row] * inv_h + eps);
+      const T* sr = s + row * ss_;
+      T* yr = y + row * sy;
+      for (int j = tail0; j < shard; j += kStreamBlock) yr[j] = from_f32<T>((to_f32(sr[j]) * rs) * to_f32(w[j]));
+    }
   }
 }
 
@@ -542,27 +554,41 @@ hipError_t run_shard_partial(const RmsShardArgs& a, hipStream_t stream) {
   return hipSuccess;
 }
 
-template <typename T, typename W>
-hipError_t run_shard_apply(const RmsShardArgs& a, hipStream_t stream) {
-  const int64_t cap = max_blocks_per_launch(kStreamBlock);
+template <typename T, typename W, int R>
+hipError_t run_shard_apply_r(const RmsShardArgs& a, hipStream_t stream) {
+  const int64_t cap = max_blocks_per_launch(kStreamBlock) * R;  // rows per launch
   const float inv_h = 1.0f / static_cast<float>(a.hidden);
   for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
-    const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
+    const int64_t end = std::min(a.rows, r0 + cap);
+    const dim3 grid(static_cast<unsigned>(ceil_div(end - r0, R)));
     if (a.vector_ok) {
-      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 16 / sizeof(T)>), grid, dim3(kStreamBlock), 0,
+      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 16 / sizeof(T), R>), grid, dim3(kStreamBlock), 0,
                          stream, static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
-                         static_cast<T*>(a.y), r0, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                         static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
                          a.eps);
     } else {
-      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 1>), grid, dim3(kStreamBlock), 0, stream,
+      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 1, R>), grid, dim3(kStreamBlock), 0, stream,
                          static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
-                         static_cast<T*>(a.y), r0, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                         static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
                          a.eps);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   return hipSuccess;
+}
+
+#ifndef AKO_TP_APPLY_ROWS
+#define AKO_TP_APPLY_ROWS 2
+#endif
+
+// Rows per workgroup: R for launches with enough rows to fill the chip many
+// times over, 1 for decode-sized ones (which need every workgroup they can get).
+template <typename T, typename W>
+hipError_t run_shard_apply(const RmsShardArgs& a, hipStream_t stream) {
+  if (AKO_TP_APPLY_ROWS >= 4 && a.rows >= 4096) return run_shard_apply_r<T, W, 4>(a, stream);
+  if (AKO_TP_APPLY_ROWS >= 2 && a.rows >= 4096) return run_shard_apply_r<T, W, 2>(a, stream);
+  return run_shard_apply_r<T, W, 1>(a, stream);
 }
 
 }  // namespace

@@ -78,12 +78,14 @@ def test_shard_abi_validation() -> None:
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows,hidden,shards", [
     (rows, hidden, shards)
-    for rows, hidden in [(1, 4096), (33, 16384), (16384, 16384), (5, 4100)]
+    for rows, hidden in [(1, 4096), (33, 16384), (16384, 16384), (4097, 2048), (5, 4100)]
     for shards in (1, 2, 8) if hidden % shards == 0
 ])
 def test_hip_slices_compose_to_the_full_row(rows: int, hidden: int, shards: int, dtype) -> None:
     """configs[1] rows and widths cut into 1, 2 or 8 slices (TP=8 puts 2048 of
-    16384 on a rank); 4100/2 slices are not 16-byte aligned (scalar path)."""
+    16384 on a rank); 4097 rows leave the apply kernel's last workgroup (two
+    rows each from 4096 rows on) one row; 4100/2 slices are not 16-byte
+    aligned (scalar path)."""
     dev = "cuda"
     x, r = drandn((rows, hidden), dtype, 4), drandn((rows, hidden), dtype, 5)
     w = drandn((hidden,), dtype, 6, scale=0.1, shift=1.0)
