@@ -1,10 +1,14 @@
 """Randomised GPU parity sweep: seeded random shapes, padded strides, dtypes
 and weight / table dtypes for every HIP kernel, each case against the numpy
 oracle (at most 2 ulp of max|ref| for fp16/bf16, 4 for fp32; the rounded
-residual sum bit for bit). Deterministic: the cases come from fixed seeds.
+residual sum bit for bit). Deterministic: the cases come from fixed seeds,
+4-6 per test by default; AKO_RANDOM_SEEDS=N runs seeds 0..N-1 of each for a
+wider sweep.
 """
 
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -23,6 +27,11 @@ DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 MAX_ULPS = {torch.float16: 2.0, torch.bfloat16: 2.0, torch.float32: 4.0}
 
 
+def seeds(default: int) -> range:
+    """Seeds 0..default-1, or 0..AKO_RANDOM_SEEDS-1 when that is set."""
+    return range(int(os.environ.get("AKO_RANDOM_SEEDS", default)))
+
+
 def _check(expected: np.ndarray, got: torch.Tensor, dtype: torch.dtype, case: str) -> None:
     rep = oracle.gate(expected, to_np(got), NAMES[dtype])
     assert rep["passed"] and rep["err_ulps"] <= MAX_ULPS[dtype], (case, rep)
@@ -33,7 +42,7 @@ def _padded(rows: int, width: int, pad: int, dtype: torch.dtype, gen: torch.Gene
     return base[:, :width]
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", seeds(6))
 def test_rmsnorm_random_cases(seed: int) -> None:
     rng = np.random.default_rng(1000 + seed)
     gen = torch.Generator(device=DEV).manual_seed(seed)
@@ -57,7 +66,7 @@ def test_rmsnorm_random_cases(seed: int) -> None:
         _check(ey, y, dtype, case)
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", seeds(6))
 def test_rope_random_cases(seed: int) -> None:
     rng = np.random.default_rng(2000 + seed)
     gen = torch.Generator(device=DEV).manual_seed(seed)
@@ -77,7 +86,7 @@ def test_rope_random_cases(seed: int) -> None:
                rope_hip(x, cos, sin, style), dtype, case)
 
 
-@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("seed", seeds(4))
 def test_rope_qk_cache_random_cases(seed: int) -> None:
     rng = np.random.default_rng(3000 + seed)
     gen = torch.Generator(device=DEV).manual_seed(seed)
@@ -105,7 +114,7 @@ def test_rope_qk_cache_random_cases(seed: int) -> None:
         np.testing.assert_array_equal(to_np(vc), ev, err_msg=case)
 
 
-@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("seed", seeds(4))
 def test_swiglu_random_cases(seed: int) -> None:
     rng = np.random.default_rng(4000 + seed)
     gen = torch.Generator(device=DEV).manual_seed(seed)
