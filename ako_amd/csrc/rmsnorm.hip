@@ -377,6 +377,9 @@ __global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_apply(
 
 namespace {
 
+// Launches of at most this many rows leave CUs without a workgroup (256 CUs).
+constexpr int64_t kFewRows = 256;
+
 struct RegShape {
   int wpr, vpt;
 };
@@ -395,13 +398,20 @@ constexpr int kMaxRegPackets = 16 * 64 * 8;
 // two tensors per packet, with one packet per lane over 8-16 wavefronts.
 // Rows that fit one wavefront's first packet stay on one wavefront so that
 // small rows need no LDS exchange and pack 4 rows per workgroup.
-RegShape pick_shape(int64_t nvec, bool residual) {
+RegShape pick_shape(int64_t nvec, bool residual, int64_t rows) {
+  // One packet per lane and more wavefronts per row for the residual variant,
+  // and for plain rows when a launch has too few rows to give every CU a
+  // workgroup (decode): then each row's latency is the launch's. Graph-replayed
+  // on MI355X, plain rows of 4096 half elements take 1.89 us as (8, 1) against
+  // 2.13 us as (4, 2) at 1 row (2.04 against 2.28 at 32 rows); at 16384 rows
+  // (4, 2) is the faster.
+  const bool one_packet = residual || rows <= kFewRows;
   RegShape s{16, 8};
   if (nvec <= 64) s = {1, 1};
   else if (nvec <= 128) s = {1, 2};
   else if (nvec <= 256) s = {2, 2};
-  else if (nvec <= 512) s = residual ? RegShape{8, 1} : RegShape{4, 2};
-  else if (nvec <= 1024) s = residual ? RegShape{16, 1} : RegShape{8, 2};
+  else if (nvec <= 512) s = one_packet ? RegShape{8, 1} : RegShape{4, 2};
+  else if (nvec <= 1024) s = one_packet ? RegShape{16, 1} : RegShape{8, 2};
   else if (nvec <= 2048) s = {16, 2};
   else if (nvec <= 4096) s = {16, 4};
   const RmsTuning& tu = g_rms_tuning;
@@ -523,7 +533,7 @@ hipError_t run_typed(const RmsArgs& a, hipStream_t stream) {
   const bool reg = a.vector_ok && g_rms_tuning.force_stream == 0 && nvec <= kMaxRegPackets &&
                    nvec >= 1;
   if (!reg) return a.residual ? run_stream<T, W, true>(a, stream) : run_stream<T, W, false>(a, stream);
-  const RegShape s = pick_shape(nvec, a.residual);
+  const RegShape s = pick_shape(nvec, a.residual, a.rows);
   return a.residual ? run_reg_shape<T, W, true>(s, a, stream)
                     : run_reg_shape<T, W, false>(s, a, stream);
 }
