@@ -28,8 +28,7 @@ struct RopeTuning {
   int iters = 0;             // key 2: head chunks unrolled per loop trip
 };
 struct SwigluTuning {
-  int vecs_per_thread = 0;  // key 1
-  int block = 0;            // key 2: threads per workgroup (64..1024)
+  int vecs_per_thread = 0;  // key 1: packets per lane (1, 2, 4 or 8)
 };
 extern RmsTuning g_rms_tuning;
 extern RopeTuning g_rope_tuning;

@@ -151,11 +151,12 @@ hipError_t run_rows(const SwigluArgs& a, hipStream_t stream) {
 template <typename T>
 hipError_t run_typed(const SwigluArgs& a, hipStream_t stream) {
   constexpr int E = 16 / sizeof(T);
-  // One packet per lane for large streams (measured on MI355X: 6.57 TB/s at
-  // U=1 against 6.12 TB/s at U=4 for 16384 x 14336 bf16); two for small ones,
-  // where fewer, fuller workgroups finish sooner.
+  // One packet per lane (measured on MI355X: 6.57 TB/s at U=1 against
+  // 6.12 TB/s at U=4 for 16384 x 14336 bf16; graph-replayed decode calls at
+  // M = 1 / 16 / 256 take 1.80 / 1.79 / 4.35 us at U=1 against 1.88 / 2.00 /
+  // 4.75 us at U=2).
   int unroll = g_swiglu_tuning.vecs_per_thread;
-  if (unroll <= 0) unroll = (a.rows * a.n) / E >= (int64_t(1) << 20) ? 1 : 2;
+  if (unroll <= 0) unroll = 1;
   if (!a.vector_ok) return run_rows<T, 1, 4>(a, stream);
   if (a.contiguous) {
     if (unroll <= 1) return run_flat<T, 1>(a, stream);
