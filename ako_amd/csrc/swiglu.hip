@@ -32,7 +32,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
   } else {
     const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+    // v_rcp_f32 flushes a subnormal result, so 1 / (1 + e) is 0 once
+    // 1 + e > 2^126 (g < -87.3) although g / (1 + e) is still a normal number
+    // down to g = -88.7, where exp overflows. Above 2^64 the denominator is
+    // scaled down by 2^64 before the reciprocal and the quotient back after
+    // it, both exact.
+    const float d = 1.0f + e;
+    const bool big = d > 0x1p64f;
+    const float s = g * __builtin_amdgcn_rcpf(big ? d * 0x1p-64f : d);
+    return (big ? s * 0x1p-64f : s) * u;
   }
 }
 
