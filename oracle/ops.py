@@ -57,7 +57,8 @@ def round_to(a: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "float32":
         return a.copy()
     if dtype == "float16":
-        return a.astype(np.float16)
+        with np.errstate(over="ignore"):  # beyond 65504 rounds to inf, as IEEE narrowing does
+            return a.astype(np.float16)
     if dtype == "bfloat16":
         bits = a.view(np.uint32).astype(np.uint64)
         lsb = (bits >> 16) & 1
@@ -82,10 +83,11 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, *, dtype: str = "fl
     hidden = xf.shape[-1]
     if hidden == 0 or xf.size == 0:
         return round_to(xf, dtype)
-    sq = xf * xf
-    var = sq.sum(axis=-1, keepdims=True, dtype=np.float32) * np.float32(1.0 / hidden)
-    rstd = np.float32(1.0) / np.sqrt(var + np.float32(eps))
-    return round_to((xf * rstd) * wf, dtype)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):  # inf/NaN rows follow IEEE, as on the GPU
+        sq = xf * xf
+        var = sq.sum(axis=-1, keepdims=True, dtype=np.float32) * np.float32(1.0 / hidden)
+        rstd = np.float32(1.0) / np.sqrt(var + np.float32(eps))
+        return round_to((xf * rstd) * wf, dtype)
 
 
 def rmsnorm_residual(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float = 1e-6, *,
@@ -95,7 +97,8 @@ def rmsnorm_residual(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float = 1
     in the storage dtype (fp32 add, rounded), then normalised."""
     if np.shape(x) != np.shape(r):
         raise ValueError(f"Shape mismatch: x {np.shape(x)} vs residual {np.shape(r)}")
-    s = round_to(to_f32(x, dtype) + to_f32(r, dtype), dtype)
+    with np.errstate(over="ignore"):
+        s = round_to(to_f32(x, dtype) + to_f32(r, dtype), dtype)
     return rmsnorm(s, w, eps, dtype=dtype, w_dtype=w_dtype), s
 
 
@@ -132,13 +135,14 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, style: str = "neox", *
     c = to_f32(cos, table_dtype)[None, :, None, :]
     s = to_f32(sin, table_dtype)[None, :, None, :]
     half = xf.shape[-1] // 2
-    if style == "neox":
-        a, b = xf[..., :half], xf[..., half:]
-        out = np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
-    else:
-        a, b = xf[..., 0::2], xf[..., 1::2]
-        out = np.stack([a * c - b * s, a * s + b * c], axis=-1).reshape(xf.shape)
-    return round_to(out, dtype)
+    with np.errstate(over="ignore", invalid="ignore"):  # IEEE inf/NaN, as on the GPU
+        if style == "neox":
+            a, b = xf[..., :half], xf[..., half:]
+            out = np.concatenate([a * c - b * s, a * s + b * c], axis=-1)
+        else:
+            a, b = xf[..., 0::2], xf[..., 1::2]
+            out = np.stack([a * c - b * s, a * s + b * c], axis=-1).reshape(xf.shape)
+        return round_to(out, dtype)
 
 
 def rope_qk_cache(q: np.ndarray, k: np.ndarray, v: np.ndarray | None, cos: np.ndarray,
@@ -185,7 +189,7 @@ def swiglu(g: np.ndarray, u: np.ndarray, *, dtype: str = "float32") -> np.ndarra
     uf = to_f32(u, dtype)
     with np.errstate(over="ignore", invalid="ignore"):
         silu = gf / (np.float32(1.0) + np.exp(-gf))
-    return round_to(silu * uf, dtype)
+        return round_to(silu * uf, dtype)
 
 
 # -- the gate, for reports ----------------------------------------------------------------

@@ -438,3 +438,90 @@ def test_swiglu_every_finite_half_gate(dtype) -> None:
         assert dist.max() <= 1, (f"{dist.max()} ulp at gate {float(g[worst])} (bits {int(bits[worst]):#06x}): "
                                  f"got bits {int(got_bits[worst]):#06x}, oracle {int(ref_bits[worst]):#06x}; "
                                  f"{int((dist > 0).sum())} of {dist.size} differ")
+
+
+def _finite16(dtype) -> np.ndarray:
+    """Every finite 16-bit pattern of ``dtype`` (fp16 or bf16)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    mask = 0x7C00 if dtype == torch.float16 else 0x7F80
+    return bits[(bits & mask) != mask]
+
+
+def _bits_tensor(bits: np.ndarray, dtype) -> torch.Tensor:
+    return torch.from_numpy(bits.view(np.int16).copy()).to(DEV).view(dtype)
+
+
+def _ulp_dist(got: torch.Tensor, ref: np.ndarray) -> np.ndarray:
+    """Element-wise distance in ulps; two NaNs (of any sign or payload) are 0
+    apart, a NaN and a number 65536."""
+    got_bits = got.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    ref_bits = (ref.view(np.uint16) if ref.dtype != np.uint16 else ref).reshape(-1)
+    exp_mask = 0x7C00 if got.dtype == torch.float16 else 0x7F80
+
+    def nan(b: np.ndarray) -> np.ndarray:
+        return ((b & exp_mask) == exp_mask) & ((b & ~np.uint16(0x8000 | exp_mask)) != 0)
+
+    dist = np.abs(_ordered16(got_bits) - _ordered16(ref_bits))
+    gn, rn = nan(got_bits), nan(ref_bits)
+    return np.where(gn & rn, 0, np.where(gn ^ rn, 65536, dist))
+
+
+@pytest.mark.parametrize("style", ["neox", "interleaved"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rope_every_finite_half_value(dtype, style) -> None:
+    """Every finite 16-bit value as the first and as the second element of a
+    rotated pair, at 255 positions with tables in the input dtype: the kernel
+    rounds the same fp32 products and sums as the oracle, element by element
+    within 1 ulp."""
+    bits = _finite16(dtype)
+    n = bits.size  # 63488 (fp16) or 65280 (bf16)
+    heads = n // (255 * 128) if n % (255 * 128) == 0 else None
+    rng = np.random.default_rng(31)
+    cos, sin = build_rope_tables(256, 128, device=DEV)
+    cos, sin = cos.to(dtype), sin.to(dtype)
+    for perm in (np.arange(n), rng.permutation(n)):
+        flat = bits[perm]
+        pad = (-flat.size) % (256 * 128)
+        flat = np.concatenate([flat, np.zeros(pad, dtype=np.uint16)])
+        x = _bits_tensor(flat, dtype).view(1, 256, -1, 128)
+        y = rope_hip(x, cos, sin, style)
+        ref = oracle.rope(to_np(x), to_np(cos), to_np(sin), style, dtype=NAMES[dtype], table_dtype=NAMES[dtype])
+        dist = _ulp_dist(y, ref)
+        assert dist.max() <= 1, f"{dist.max()} ulp; {int((dist > 0).sum())} of {dist.size} differ"
+    assert heads is None or heads >= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rmsnorm_extreme_rows(dtype) -> None:
+    """Rows of subnormals, rows near the format's maximum (whose sum of squares
+    overflows fp32 for bf16), a single non-zero element, zeros, and mixes,
+    plain and residual: element by element within 1 ulp of the oracle (the
+    rounded residual sum exactly)."""
+    rng = np.random.default_rng(37)
+    h = 4096
+    if dtype == torch.float16:
+        sub, big = (0x0001, 0x03FF), (0x7800, 0x7BFF)   # subnormals; 32768 .. 65504
+    else:
+        sub, big = (0x0001, 0x007F), (0x7E00, 0x7F7F)   # subnormals; 4.3e37 .. 3.4e38
+    rows = []
+    for lo, hi in (sub, big):
+        for sign in (0, 0x8000):
+            rows.append(rng.integers(lo, hi + 1, h, dtype=np.uint32).astype(np.uint16) | np.uint16(sign))
+    one = np.zeros(h, dtype=np.uint16)
+    one[rng.integers(h)] = 0x3C00 if dtype == torch.float16 else 0x3F80  # a single 1.0
+    rows += [one, np.zeros(h, dtype=np.uint16)]
+    mix = rng.integers(sub[0], sub[1] + 1, h, dtype=np.uint32).astype(np.uint16)
+    mix[::97] = rng.integers(big[0], big[1] + 1, mix[::97].size, dtype=np.uint32).astype(np.uint16)
+    rows.append(mix)
+    x = _bits_tensor(np.stack(rows), dtype)
+    r = _bits_tensor(np.stack(rows[::-1]), dtype)
+    w = grandn((h,), dtype, 41, scale=0.1, shift=1.0)
+    for eps in (1e-6, 0.0):
+        y = rmsnorm_hip(x, w, eps)
+        dist = _ulp_dist(y, oracle.rmsnorm(to_np(x), to_np(w), eps, dtype=NAMES[dtype]))
+        assert dist.max() <= 1, f"plain eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+        y, s = rmsnorm_residual_hip(x, r, w, eps)
+        ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), eps, dtype=NAMES[dtype])
+        assert _ulp_dist(s, es).max() == 0
+        dist = _ulp_dist(y, ey)
+        assert dist.max() <= 1, f"residual eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
