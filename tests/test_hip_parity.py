@@ -525,3 +525,45 @@ def test_rmsnorm_extreme_rows(dtype) -> None:
         assert _ulp_dist(s, es).max() == 0
         dist = _ulp_dist(y, ey)
         assert dist.max() <= 1, f"residual eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+
+
+def _ordered32(a: np.ndarray) -> np.ndarray:
+    b = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.int64)
+    return np.where(b & 0x80000000, 0x80000000 - (b & 0x7FFFFFFF), 0x80000000 + b)
+
+
+def _ulp_dist32(got: np.ndarray, ref: np.ndarray) -> np.ndarray:
+    got, ref = np.asarray(got, np.float32).reshape(-1), np.asarray(ref, np.float32).reshape(-1)
+    dist = np.abs(_ordered32(got) - _ordered32(ref))
+    gn, rn = np.isnan(got), np.isnan(ref)
+    return np.where(gn & rn, 0, np.where(gn ^ rn, 1 << 32, dist))
+
+
+def test_fp32_extremes_element_by_element() -> None:
+    """fp32 RMSNorm (rows of subnormals, of values near 1e38 whose squares
+    overflow, a single non-zero element, zeros) and fp32 SwiGLU over gates
+    from -100 to 100 including subnormals: within 4 ulp of the oracle element
+    by element (the fp32 target)."""
+    rng = np.random.default_rng(43)
+    h = 4096
+    rows = [
+        rng.uniform(1e-41, 1e-39, h) * rng.choice([-1, 1], h),  # subnormal
+        rng.uniform(1e37, 3e38, h) * rng.choice([-1, 1], h),    # squares overflow
+        np.zeros(h),
+        rng.standard_normal(h) * 1e-20,
+    ]
+    one = np.zeros(h)
+    one[rng.integers(h)] = 1.0
+    rows.append(one)
+    x = torch.tensor(np.stack(rows), dtype=torch.float32, device=DEV)
+    w = grandn((h,), torch.float32, 47, scale=0.1, shift=1.0)
+    for eps in (1e-6, 0.0):
+        ref = oracle.rmsnorm(to_np(x), to_np(w), eps, dtype="float32")
+        dist = _ulp_dist32(to_np(rmsnorm_hip(x, w, eps)), ref)
+        assert dist.max() <= 4, f"rmsnorm eps={eps}: {dist.max()} ulp"
+    g = torch.tensor(np.concatenate([np.linspace(-100, 100, 200001), [1e-40, -1e-40, 0.0, -0.0, 1e-30]]),
+                     dtype=torch.float32, device=DEV)
+    u = grandn(g.shape, torch.float32, 53)
+    ref = oracle.swiglu(to_np(g), to_np(u), dtype="float32")
+    dist = _ulp_dist32(to_np(swiglu_hip(g, u)), ref)
+    assert dist.max() <= 4, f"swiglu: {dist.max()} ulp at g={float(g[int(np.argmax(dist))])}"
