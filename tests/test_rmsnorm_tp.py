@@ -176,3 +176,29 @@ def test_two_ranks_on_the_gpu_compose_to_the_full_row(tmp_path, dtype) -> None:
     """The HIP halves in two processes sharing cuda:0; the partial sums cross
     gloo through host copies (4096 rows x 8192, each rank a 4096-wide slice)."""
     _run_ranks(tmp_path, 2, "cuda:0", dtype, 4096, 8192, use_hip=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
+def test_hip_slices_extreme_rows() -> None:
+    """Rows of subnormals, of values whose squares overflow fp32, zeros and a
+    single non-zero element, cut into 4 slices: the composed result equals the
+    full-row oracle element by element within 1 ulp, NaN where it is NaN."""
+    from tests.test_hip_parity import _ulp_dist
+
+    rng = np.random.default_rng(59)
+    h = 4096
+    rows = [rng.integers(0x0001, 0x0080, h, dtype=np.uint32).astype(np.uint16),
+            rng.integers(0x7E00, 0x7F80, h, dtype=np.uint32).astype(np.uint16) | np.uint16(0x8000),
+            np.zeros(h, dtype=np.uint16)]
+    one = np.zeros(h, dtype=np.uint16)
+    one[rng.integers(h)] = 0x3F80
+    rows.append(one)
+    bits = np.stack(rows)
+    x = torch.from_numpy(bits.view(np.int16).copy()).cuda().view(torch.bfloat16)
+    r = torch.from_numpy(bits[::-1].copy().view(np.int16)).cuda().view(torch.bfloat16)
+    w = drandn((h,), torch.bfloat16, 61, scale=0.1, shift=1.0)
+    y, s = rmsnorm_sharded(x, r, w, 1e-6, shards=4)
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), 1e-6, dtype="bfloat16")
+    assert _ulp_dist(s, es).max() == 0
+    assert _ulp_dist(y, ey).max() <= 1
