@@ -567,3 +567,35 @@ def test_fp32_extremes_element_by_element() -> None:
     ref = oracle.swiglu(to_np(g), to_np(u), dtype="float32")
     dist = _ulp_dist32(to_np(swiglu_hip(g, u)), ref)
     assert dist.max() <= 4, f"swiglu: {dist.max()} ulp at g={float(g[int(np.argmax(dist))])}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_element_by_element_at_config_shapes(dtype) -> None:
+    """Element-wise distance to the oracle, which is tighter than the gate's
+    max|ref|-relative budget. Half precision: at most 1 ulp for RMSNorm and
+    SwiGLU, RoPE bit-exact. fp32: RMSNorm within 4 ulp (a different summation
+    order moves rstd by a few ulp), RoPE bit-exact, SwiGLU within 8 ulp
+    (device expf against numpy's exp)."""
+    half = dtype != torch.float32
+
+    def dist(y, ref):
+        return _ulp_dist(y, ref) if half else _ulp_dist32(to_np(y), ref)
+
+    for rows, h in ((1, 4096), (32, 8192), (16384, 16384)):
+        x, r = grandn((rows, h), dtype, 0), grandn((rows, h), dtype, 2)
+        w = grandn((h,), dtype, 1, scale=0.1, shift=1.0)
+        sel = torch.as_tensor(sample_rows(rows), device=DEV)
+        d = dist(rmsnorm_hip(x, w, 1e-6)[sel], oracle.rmsnorm(to_np(x[sel]), to_np(w), 1e-6, dtype=NAMES[dtype]))
+        assert d.max() <= (1 if half else 4), (rows, h, int(d.max()))
+        y, s = rmsnorm_residual_hip(x, r, w, 1e-6)
+        ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), 1e-6, dtype=NAMES[dtype])
+        assert dist(s[sel], es).max() == 0
+        assert dist(y[sel], ey).max() <= (1 if half else 4), (rows, h)
+    cos, sin = build_rope_tables(2048, 128, device=DEV)
+    for tdt in {torch.float32, dtype}:
+        q = grandn((2, 2048, 32, 128), dtype, 5)
+        ref = oracle.rope(to_np(q), to_np(cos.to(tdt)), to_np(sin.to(tdt)), dtype=NAMES[dtype], table_dtype=NAMES[tdt])
+        assert dist(rope_hip(q, cos.to(tdt), sin.to(tdt)), ref).max() == 0
+    g, u = grandn((512, 14336), dtype, 7, scale=3.0), grandn((512, 14336), dtype, 8)
+    d = dist(swiglu_hip(g, u), oracle.swiglu(to_np(g), to_np(u), dtype=NAMES[dtype]))
+    assert d.max() <= (1 if half else 8), int(d.max())
