@@ -301,6 +301,7 @@ int ako_rmsnorm_shard_apply_fwd(const void* s, const void* w, const float* total
 }
 
 // ------------------------------------------------------------------- RoPE --
+extern "C++" {  // C++ helpers inside the C-linkage block
 namespace {
 
 struct RopeTensorIn {
@@ -454,6 +455,7 @@ int rope_common(const char* fn, const RopeTensorIn* ts, int nt, const void* cos,
 }
 
 }  // namespace
+}  // extern "C++"
 
 int ako_rope_fwd(const void* x, const void* cos_table, const void* sin_table, void* y,
                  int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int64_t x_stride_b,

@@ -161,11 +161,11 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
     } else {
       P o;
 #pragma unroll
-      for (int p = 0; p < E / 2; ++p) {
-        const float x0 = to_f32(lo[it].e[2 * p]);
-        const float x1 = to_f32(lo[it].e[2 * p + 1]);
-        o.e[2 * p] = from_f32<T>(x0 * c[p] - x1 * n[p]);
-        o.e[2 * p + 1] = from_f32<T>(x0 * n[p] + x1 * c[p]);
+      for (int i = 0; i < E / 2; ++i) {
+        const float x0 = to_f32(lo[it].e[2 * i]);
+        const float x1 = to_f32(lo[it].e[2 * i + 1]);
+        o.e[2 * i] = from_f32<T>(x0 * c[i] - x1 * n[i]);
+        o.e[2 * i + 1] = from_f32<T>(x0 * n[i] + x1 * c[i]);
       }
       store_pack<T, E, true>(dst[it], o);
     }
