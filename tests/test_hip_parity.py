@@ -606,3 +606,45 @@ def test_element_by_element_at_config_shapes(dtype) -> None:
     g, u = grandn((512, 14336), dtype, 7, scale=3.0), grandn((512, 14336), dtype, 8)
     d = dist(swiglu_hip(g, u), oracle.swiglu(to_np(g), to_np(u), dtype=NAMES[dtype]))
     assert d.max() <= (1 if half else 8), int(d.max())
+
+
+def test_tensors_beyond_2_31_elements() -> None:
+    """Each kernel on a tensor of more than 2^31 elements (over 4 GiB in
+    fp16), so element offsets need 64 bits: the last rows / tokens and a
+    seeded sample against the oracle (RoPE bit for bit, the residual sum
+    exactly, the rest within 1 ulp element by element)."""
+    rng = np.random.default_rng(71)
+
+    def pick(n: int) -> torch.Tensor:
+        idx = np.unique(np.concatenate([[0, n - 3, n - 2, n - 1], rng.choice(n, 40, replace=False)]))
+        return torch.as_tensor(idx, device=DEV)
+
+    rows = (1 << 31) // 8192 + 3
+    x, r = grandn((rows, 8192), torch.float16, 70), grandn((rows, 8192), torch.float16, 72)
+    w = grandn((8192,), torch.float16, 74, scale=0.1, shift=1.0)
+    assert x.numel() > (1 << 31)
+    y, s = rmsnorm_residual_hip(x, r, w, 1e-6)
+    sel = pick(rows)
+    ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), 1e-6, dtype="float16")
+    np.testing.assert_array_equal(to_np(s[sel]), es)
+    assert _ulp_dist(y[sel], ey).max() <= 1
+    del x, r, y, s
+    torch.cuda.empty_cache()
+
+    m = (1 << 31) // 14336 + 2
+    g, u = grandn((m, 14336), torch.bfloat16, 76), grandn((m, 14336), torch.bfloat16, 78)
+    y = swiglu_hip(g, u)
+    sel = pick(m)
+    assert _ulp_dist(y[sel], oracle.swiglu(to_np(g[sel]), to_np(u[sel]), dtype="bfloat16")).max() <= 1
+    del g, u, y
+    torch.cuda.empty_cache()
+
+    seq = (1 << 31) // (128 * 128) + 2
+    x = grandn((1, seq, 128, 128), torch.float16, 80)
+    cos, sin = build_rope_tables(seq, 128, device=DEV)
+    y = rope_hip(x, cos, sin)
+    sel = pick(seq)
+    expected = oracle.rope(to_np(x[:, sel]), to_np(cos[sel]), to_np(sin[sel]), "neox", dtype="float16")
+    np.testing.assert_array_equal(to_np(y[:, sel]), expected)
+    del x, y
+    torch.cuda.empty_cache()
