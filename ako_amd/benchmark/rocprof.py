@@ -145,23 +145,52 @@ def read_kernel_trace(path: Path) -> list[tuple[str, int, int]]:
     return sorted(rows, key=lambda r: r[1])
 
 
-def durations_by_grid(path: Path, skip: int = 0) -> list[dict[str, Any]]:
+def durations_by_grid(path: Path, skip: int = 0, *, run_gap_ms: float | None = None,
+                      min_calls: int = 1) -> list[dict[str, Any]]:
     """Kernel durations of a ``*_kernel_trace.csv`` grouped by (kernel, workgroup
     size, grid size): one group per launch shape, so the cells of a benchmark
     that share a kernel but not a shape come apart. ``skip`` drops each group's
-    first launches (warm-up)."""
-    groups: dict[tuple[str, int, int], list[int]] = {}
+    first launches (warm-up).
+
+    A kernel compiled for dynamic shapes (a ``torch.compile(dynamic=True)``
+    reduction, one program per row) can launch the same grid for rows of
+    different widths. With ``run_gap_ms`` each group is further split into
+    runs: a launch that starts more than ``run_gap_ms`` after the previous
+    launch of its group begins a new run, so the back-to-back launches of one
+    benchmarked cell stay together (``run`` numbers them in time order, from
+    1). ``skip`` then applies per run, and runs left with fewer than
+    ``min_calls`` launches (a lone correctness call) are dropped."""
+    groups: dict[tuple[str, int, int], list[tuple[int, int]]] = {}
     with open(path, newline="") as fh:
         for r in csv.DictReader(fh):
             key = (r["Kernel_Name"], int(r["Workgroup_Size_X"]), int(r["Grid_Size_X"]))
-            groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            start = int(r["Start_Timestamp"])
+            groups.setdefault(key, []).append((start, int(r["End_Timestamp"]) - start))
     out = []
-    for (name, wg, grid), ns in groups.items():
-        ns = ns[skip:] if len(ns) > skip else ns
-        out.append({"name": name, "workgroup": wg, "grid": grid, "calls": len(ns),
-                    "median_us": statistics.median(ns) / 1e3, "mean_us": statistics.fmean(ns) / 1e3,
-                    "min_us": min(ns) / 1e3})
-    return sorted(out, key=lambda g: (g["name"], g["grid"], g["workgroup"]))
+    for (name, wg, grid), launches in groups.items():
+        launches.sort()
+        runs: list[list[int]] = [[]]
+        for i, (start, ns) in enumerate(launches):
+            if run_gap_ms is not None and i > 0 and start - launches[i - 1][0] > run_gap_ms * 1e6:
+                runs.append([])
+            runs[-1].append(ns)
+        for number, ns in enumerate(runs, 1):
+            ns = ns[skip:] if len(ns) > skip else ns
+            if run_gap_ms is not None and len(ns) < min_calls:
+                continue
+            g = {"name": name, "workgroup": wg, "grid": grid, "calls": len(ns),
+                 "median_us": statistics.median(ns) / 1e3, "mean_us": statistics.fmean(ns) / 1e3,
+                 "min_us": min(ns) / 1e3}
+            if run_gap_ms is not None:
+                g["run"] = number
+            out.append(g)
+    return sorted(out, key=lambda g: (g["name"], g["grid"], g["workgroup"], g.get("run", 0)))
+
+
+def name_matches(name: str, name_filter: str | None) -> bool:
+    """True when ``name_filter`` is unset or one of its comma-separated parts
+    occurs in ``name``."""
+    return not name_filter or any(part and part in name for part in name_filter.split(","))
 
 
 def grid_markdown(groups: list[dict[str, Any]], command: str, title: str, note: str = "",
@@ -169,13 +198,16 @@ def grid_markdown(groups: list[dict[str, Any]], command: str, title: str, note: 
     lines = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
     if note:
         lines += [note, ""]
-    lines += ["| kernel | workgroup | grid (work-items) | calls | median us | mean us | min us |",
-              "|---|---:|---:|---:|---:|---:|---:|"]
+    runs = any("run" in g for g in groups)
+    lines += ["| kernel | workgroup | grid (work-items) | " + ("run | " if runs else "")
+              + "calls | median us | mean us | min us |",
+              "|---|---:|---:|" + ("---:|" if runs else "") + "---:|---:|---:|---:|"]
     for g in groups:
-        if name_filter and name_filter not in g["name"]:
+        if not name_matches(g["name"], name_filter):
             continue
         name = g["name"] if len(g["name"]) <= 90 else g["name"][:87] + "..."
-        lines.append(f"| `{name}` | {g['workgroup']} | {g['grid']} | {g['calls']} | {g['median_us']:.2f} | "
+        run = f"{g['run']} | " if runs else ""
+        lines.append(f"| `{name}` | {g['workgroup']} | {g['grid']} | {run}{g['calls']} | {g['median_us']:.2f} | "
                      f"{g['mean_us']:.2f} | {g['min_us']:.2f} |")
     return "\n".join(lines) + "\n"
 
@@ -279,7 +311,12 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--by-grid", action="store_true",
                     help="with --trace: durations per (kernel, workgroup, grid) instead of a tail breakdown")
     ap.add_argument("--skip", type=int, default=0, help="with --by-grid: warm-up launches dropped per group")
-    ap.add_argument("--filter", default=None, help="with --by-grid: only kernels whose name contains this")
+    ap.add_argument("--filter", default=None,
+                    help="with --by-grid: only kernels whose name contains this (or one of several, comma-separated)")
+    ap.add_argument("--run-gap-ms", type=float, default=None,
+                    help="with --by-grid: split each group into runs at start gaps above this many ms")
+    ap.add_argument("--min-calls", type=int, default=1,
+                    help="with --run-gap-ms: drop runs with fewer launches (after --skip)")
     ap.add_argument("--tail-ms", type=float, default=None, help="with --trace: window at the end of the run")
     ap.add_argument("--steps", type=int, default=None, help="with --trace: steps inside the window")
     ap.add_argument("--marker", default=None, help="with --trace: a kernel launched once per step")
@@ -293,9 +330,8 @@ def main(argv: list[str] | None = None) -> int:
         args.md.write_text(counters_markdown(cells, args.command, args.title, args.note))
         record: dict[str, Any] = {"kind": "counters_by_cell", "title": args.title, "cells": cells}
     elif args.trace and args.by_grid:
-        groups = durations_by_grid(args.trace, args.skip)
-        if args.filter:
-            groups = [g for g in groups if args.filter in g["name"]]
+        groups = durations_by_grid(args.trace, args.skip, run_gap_ms=args.run_gap_ms, min_calls=args.min_calls)
+        groups = [g for g in groups if name_matches(g["name"], args.filter)]
         args.md.write_text(grid_markdown(groups, args.command, args.title, args.note))
         record = {"kind": "durations_by_grid", "title": args.title, "groups": groups}
     elif args.trace:

@@ -139,3 +139,41 @@ def test_durations_by_grid_separate_launch_shapes(tmp_path) -> None:
     assert rocprof.main(["--trace", str(trace), "--by-grid", "--skip", "1", "--md", str(out),
                          "--json", str(tmp_path / "g.json")]) == 0
     assert json.loads((tmp_path / "g.json").read_text())["kind"] == "durations_by_grid"
+
+
+def test_durations_by_grid_split_into_runs(tmp_path) -> None:
+    """A dynamic-shape kernel that launches one grid for two row widths: runs
+    separated by a start gap come apart, warm-up drops per run, and a lone
+    correctness launch is dropped by ``min_calls``."""
+    trace = tmp_path / "t.csv"
+    fields = ["Kernel_Name", "Workgroup_Size_X", "Grid_Size_X", "Start_Timestamp", "End_Timestamp"]
+    launches = [(0, 500_000)]  # a lone gate call, then two benchmarked cells
+    t = 20_000_000
+    for dur_ns in (150_000, 100_000, 100_000, 110_000):  # narrow rows
+        launches.append((t, dur_ns))
+        t += 300_000
+    t += 20_000_000
+    for dur_ns in (300_000, 200_000, 220_000, 200_000):  # wide rows, same grid
+        launches.append((t, dur_ns))
+        t += 600_000
+    with open(trace, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=fields)
+        w.writeheader()
+        for start, dur in launches:
+            w.writerow({"Kernel_Name": "triton_red_fused_x", "Workgroup_Size_X": 512, "Grid_Size_X": 8192,
+                        "Start_Timestamp": start, "End_Timestamp": start + dur})
+        w.writerow({"Kernel_Name": "other", "Workgroup_Size_X": 64, "Grid_Size_X": 64,
+                    "Start_Timestamp": 5, "End_Timestamp": 6})
+    groups = rocprof.durations_by_grid(trace, skip=1, run_gap_ms=5.0, min_calls=2)
+    mine = [g for g in groups if g["name"] == "triton_red_fused_x"]
+    assert [(g["run"], g["calls"]) for g in mine] == [(2, 3), (3, 3)]
+    assert mine[0]["median_us"] == pytest.approx(100.0) and mine[1]["median_us"] == pytest.approx(200.0)
+    # Without run splitting the two widths would share one median.
+    whole = [g for g in rocprof.durations_by_grid(trace, skip=1) if g["name"] == "triton_red_fused_x"]
+    assert len(whole) == 1 and "run" not in whole[0]
+    md = rocprof.grid_markdown(groups, "cmd", "t", name_filter="triton,ako")
+    assert "| `triton_red_fused_x` | 512 | 8192 | 3 | 3 | 200.00 | 206.67 |" in md and "`other`" not in md
+    out = tmp_path / "g.md"
+    assert rocprof.main(["--trace", str(trace), "--by-grid", "--skip", "1", "--run-gap-ms", "5",
+                         "--min-calls", "2", "--filter", "triton,ako", "--md", str(out)]) == 0
+    assert "| run |" in out.read_text()
