@@ -26,7 +26,8 @@ oracle function      reference                                   pinned by
                      ``:84-93``), heads-major cache              out-of-range slots dropped; planted
                                                                  wrong-slot / wrong-row mistakes caught
 ``swiglu``           ``ako/ops/swiglu_ref.py:16-32``             zero-up -> 0; silu closed form in fp64;
-                                                                 first-order error bound
+                                                                 first-order error bound; fp32 silu
+                                                                 within 2 ulp of float64 over [-87, 87]
 ===================  ==========================================  =========
 
 Storage formats: fp32 arrays are ``float32``, fp16 arrays ``float16``, and
@@ -182,13 +183,21 @@ def rope_qk_cache(q: np.ndarray, k: np.ndarray, v: np.ndarray | None, cos: np.nd
 
 def swiglu(g: np.ndarray, u: np.ndarray, *, dtype: str = "float32") -> np.ndarray:
     """``swiglu_ref`` (swiglu_ref.py:29-32): ``silu(g) * u`` in fp32 with
-    ``silu(g) = g / (1 + exp(-g))``, narrowed to the storage dtype."""
+    ``silu(g) = g / (1 + exp(-g))``, narrowed to the storage dtype.
+
+    ``exp`` is the correctly rounded fp32 exponential: evaluated in float64
+    and rounded once to fp32 (overflowing to inf past the fp32 range). The
+    reference's ``F.silu`` calls a 1-ulp fp32 ``exp`` on either device, so the
+    correctly rounded value is the one both sides approximate. numpy's own
+    float32 ``exp`` is not used: it is up to 2 ulp from the correctly rounded
+    value and depends on the host CPU's SIMD code path."""
     if np.shape(g) != np.shape(u):
         raise ValueError(f"Shape mismatch: gate {np.shape(g)} vs up {np.shape(u)}")
     gf = to_f32(g, dtype)
     uf = to_f32(u, dtype)
     with np.errstate(over="ignore", invalid="ignore"):
-        silu = gf / (np.float32(1.0) + np.exp(-gf))
+        e = np.exp(-gf.astype(np.float64)).astype(np.float32)
+        silu = gf / (np.float32(1.0) + e)
         return round_to(silu * uf, dtype)
 
 

@@ -273,6 +273,26 @@ def test_swiglu_known_answers_and_zero() -> None:
         ops.swiglu(np.zeros((2, 8), np.float32), np.zeros((2, 16), np.float32))
 
 
+def test_swiglu_fp32_within_two_ulp_of_float64() -> None:
+    """fp32 silu(g) is at most 2 ulp from the float64 value rounded to fp32,
+    over [-87, 87] (exp overflows fp32 beyond). Three correctly rounded steps
+    (exp, 1 + e, the division) stay within that; numpy's float32 ``exp`` in
+    their place, up to 2 ulp off by itself, reaches 3 ulp here."""
+    def ordered(a: np.ndarray) -> np.ndarray:
+        i = a.view(np.int32).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+
+    g = np.linspace(-87.0, 87.0, 1_400_001).astype(np.float32)
+    g64 = g.astype(np.float64)
+    truth = (g64 / (1.0 + np.exp(-g64))).astype(np.float32)
+    got = ops.swiglu(g, np.ones_like(g))
+    assert np.abs(ordered(got) - ordered(truth)).max() <= 2
+    # Deep in the negative range 1 + e rounds to e: one division of g by the
+    # exponential, so any error there is the exponential's own.
+    neg = g < -17
+    assert np.abs(ordered(got[neg]) - ordered(truth[neg])).max() <= 2
+
+
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_swiglu_first_order_bound(dtype: str) -> None:
     """Reference tests/test_numerical_bounds.py:140-151: the half-precision result is
