@@ -110,15 +110,24 @@ def rope_tables(seq_len: int, head_dim: int, *, base: float = 10000.0, offset: i
                 dtype: str = "float32") -> tuple[np.ndarray, np.ndarray]:
     """``build_rope_tables`` (rope_ref.py:42-54) with fp32 angle formation:
     ``inv_freq = 1 / base ** (arange(half) * 2 / head_dim)``,
-    angles = outer(positions, inv_freq), then cos/sin narrowed to ``dtype``."""
+    angles = outer(positions, inv_freq), then cos/sin narrowed to ``dtype``.
+
+    Every step is an fp32 operation rounded once. ``pow``, ``cos`` and ``sin``
+    are the correctly rounded fp32 functions (float64 evaluation, one
+    rounding), which the reference's 1-ulp fp32 functions approximate;
+    numpy's float32 versions would tie the result to the host CPU's SIMD
+    code path."""
     if head_dim % 2:
         raise ValueError(f"head_dim must be even, got {head_dim}")
     half = head_dim // 2
     exponent = (np.arange(half, dtype=np.float32) * np.float32(2.0)) / np.float32(head_dim)
-    inv_freq = np.float32(1.0) / np.power(np.float32(base), exponent, dtype=np.float32)
+    powered = np.power(np.float64(np.float32(base)), exponent.astype(np.float64)).astype(np.float32)
+    inv_freq = np.float32(1.0) / powered
     positions = np.arange(offset, offset + seq_len, dtype=np.float32)
     angles = np.outer(positions, inv_freq).astype(np.float32)
-    return round_to(np.cos(angles), dtype), round_to(np.sin(angles), dtype)
+    a64 = angles.astype(np.float64)
+    return (round_to(np.cos(a64).astype(np.float32), dtype),
+            round_to(np.sin(a64).astype(np.float32), dtype))
 
 
 def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, style: str = "neox", *,
