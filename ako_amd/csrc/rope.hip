@@ -52,72 +52,13 @@ struct RopeDev {
   const void* sin;
   int token0;        // first token of this launch (launches split at token boundaries)
   int tokens;        // tokens in this launch
-  int chunks;        // head chunks (wavefronts) per token: chunks0 of t0, chunks1 of t1, the rest of t2
-  int chunks0;
-  int chunks1;
+  int chunks;        // head chunks (wavefronts) per token
   int seq;
   int head_dim;
   int pu_shift;      // log2(packets per unit) when a power of two, else -1
   int64_t st;
   int64_t total_tokens;  // batch * seq (scalar kernel)
 };
-
-// Everything a wavefront of the vector kernels shares: its token, its tensor
-// (a chunk never spans two tensors), the first head of its chunk and the
-// tensor's row pointers for that token. The wavefront index goes through
-// readfirstlane, so all of this lives in scalar registers and only the head
-// within the chunk and the packet within the head are per-lane values.
-struct RopeWave {
-  bool ok;          // the wavefront has a token (and, in KV-cache mode, a slot)
-  int p;            // table row (the cache slot in KV-cache mode)
-  int which;        // 0: t0, 1: t1, 2: t2 (copied)
-  int hbase;        // first head of the chunk within its tensor
-  int64_t heads;    // heads of that tensor
-  int64_t sxh, syh;
-  const char* xrow;  // x at (b, s, head 0)
-  char* yrow;        // y at (b, row, head 0), row = s or the cache slot
-};
-
-template <typename T, int TPB, bool CACHE>
-__device__ __forceinline__ RopeWave rope_wave(const RopeDev& a, int heads_per_chunk) {
-  RopeWave w{};
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * TPB +
-                                                  static_cast<int>(threadIdx.x) / kWave);
-  const int tl = wave / a.chunks;
-  w.ok = tl < a.tokens;
-  if (!w.ok) return w;
-  const int chunk = wave - tl * a.chunks;
-  const int token = a.token0 + tl;
-  const int b = token / a.seq;
-  const int s = token - b * a.seq;
-  w.p = s;
-  if constexpr (CACHE) {
-    const int64_t pp = *a.pos + s;
-    if (pp < 0 || pp >= a.cache_len) {  // out of the cache: nothing is written
-      w.ok = false;
-      return w;
-    }
-    w.p = static_cast<int>(pp);
-  }
-  w.which = chunk < a.chunks0 ? 0 : (chunk < a.chunks0 + a.chunks1 ? 1 : 2);
-  w.hbase = (chunk - (w.which == 0 ? 0 : (w.which == 1 ? a.chunks0 : a.chunks0 + a.chunks1))) * heads_per_chunk;
-  // Field by field, by value: a reference to the chosen descriptor would make
-  // the compiler fetch it with vector loads.
-  const auto pick = [&](const auto& f0, const auto& f1, const auto& f2) {
-    return w.which == 0 ? f0 : (w.which == 1 ? f1 : f2);
-  };
-  w.heads = pick(a.t0.heads, a.t1.heads, a.t2.heads);
-  w.sxh = pick(a.t0.sxh, a.t1.sxh, a.t2.sxh);
-  w.syh = pick(a.t0.syh, a.t1.syh, a.t2.syh);
-  const int64_t row = (CACHE && w.which != 0) ? w.p : s;
-  w.xrow = static_cast<const char*>(pick(a.t0.x, a.t1.x, a.t2.x)) +
-           (b * pick(a.t0.sxb, a.t1.sxb, a.t2.sxb) + s * pick(a.t0.sxs, a.t1.sxs, a.t2.sxs)) *
-               static_cast<int64_t>(sizeof(T));
-  w.yrow = static_cast<char*>(pick(a.t0.y, a.t1.y, a.t2.y)) +
-           (b * pick(a.t0.syb, a.t1.syb, a.t2.syb) + row * pick(a.t0.sys, a.t1.sys, a.t2.sys)) *
-               static_cast<int64_t>(sizeof(T));
-  return w;
-}
 
 template <typename T, typename TT, bool NEOX, int ITERS, int TPB, bool CACHE>
 __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
@@ -126,10 +67,14 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   using P = Pack<T, E>;
 
   // Wavefront w of this launch rotates head chunk (w % chunks) of token
-  // token0 + w / chunks. Wavefront and token indices are 32-bit (the host
-  // splits launches so that w < 2^24 and validates batch * seq < 2^31);
-  // element offsets are 64-bit.
+  // token0 + w / chunks. All index arithmetic is 32-bit (the host splits
+  // launches so that w < 2^24 and validates batch * seq < 2^31).
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = static_cast<int>(blockIdx.x) * TPB + static_cast<int>(threadIdx.x) / kWave;
+  const int tl = wave / a.chunks;
+  if (tl >= a.tokens) return;  // no barriers below: early exit is safe
+  const int chunk = wave - tl * a.chunks;
+  const int token = a.token0 + tl;
   const int half = a.head_dim / 2;
   const int unit = NEOX ? half : a.head_dim;  // elements one lane group covers
   const int per_unit = unit / E;              // packets per unit (<= 64, host-checked)
@@ -143,23 +88,51 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
     hl = lane / per_unit;
     heads_per_iter = kWave / per_unit;
   }
-  const RopeWave w = rope_wave<T, TPB, CACHE>(a, ITERS * heads_per_iter);
-  if (!w.ok) return;  // uniform over the wavefront; no barriers below
   if (hl >= heads_per_iter) return;
 
+  const int b = token / a.seq;
+  const int s = token - b * a.seq;
+  // Row of the tables and, in KV-cache mode, the cache slot of this token.
+  int p = s;
+  if constexpr (CACHE) {
+    const int64_t pp = *a.pos + s;
+    if (pp < 0 || pp >= a.cache_len) return;  // out of the cache: nothing is written
+    p = static_cast<int>(pp);
+  }
   float c[NT], n[NT];
-  load_f32<TT, NT>(static_cast<const TT*>(a.cos) + w.p * a.st + j * NT, c);
-  load_f32<TT, NT>(static_cast<const TT*>(a.sin) + w.p * a.st + j * NT, n);
+  load_f32<TT, NT>(static_cast<const TT*>(a.cos) + p * a.st + j * NT, c);
+  load_f32<TT, NT>(static_cast<const TT*>(a.sin) + p * a.st + j * NT, n);
 
+  const int h01 = static_cast<int>(a.t0.heads + a.t1.heads);
+  const int total = h01 + (CACHE ? static_cast<int>(a.t2.heads) : 0);
+  const int base = chunk * ITERS * heads_per_iter;
   P lo[ITERS], hi[ITERS];
   T* dst[ITERS];
+  [[maybe_unused]] bool copy[ITERS];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int hh = w.hbase + it * heads_per_iter + hl;
+    const int h = base + it * heads_per_iter + hl;
     dst[it] = nullptr;
-    if (hh < w.heads) {
-      const T* src = reinterpret_cast<const T*>(w.xrow) + hh * w.sxh + j * E;
-      dst[it] = reinterpret_cast<T*>(w.yrow) + hh * w.syh + j * E;
+    if (h < total) {
+      const bool first = h < a.t0.heads;
+      const bool third = CACHE && h >= h01;
+      // The tensor is chosen field by field, by value: the fields then come
+      // from scalar kernel-argument loads and a per-lane select. Binding a
+      // reference to the per-lane choice makes the compiler fetch the whole
+      // descriptor with vector loads, a memory round trip that every
+      // wavefront waits for before it can issue its first data load.
+      const auto pick = [&](const auto& f0, const auto& f1, const auto& f2) { return first ? f0 : (third ? f2 : f1); };
+      const void* x = pick(a.t0.x, a.t1.x, a.t2.x);
+      void* y = pick(a.t0.y, a.t1.y, a.t2.y);
+      const int64_t sxb = pick(a.t0.sxb, a.t1.sxb, a.t2.sxb), sxs = pick(a.t0.sxs, a.t1.sxs, a.t2.sxs),
+                    sxh = pick(a.t0.sxh, a.t1.sxh, a.t2.sxh);
+      const int64_t syb = pick(a.t0.syb, a.t1.syb, a.t2.syb), sys = pick(a.t0.sys, a.t1.sys, a.t2.sys),
+                    syh = pick(a.t0.syh, a.t1.syh, a.t2.syh);
+      const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
+      const int64_t srow = (CACHE && !first) ? p : s;
+      const T* src = static_cast<const T*>(x) + b * sxb + s * sxs + hh * sxh + j * E;
+      dst[it] = static_cast<T*>(y) + b * syb + srow * sys + hh * syh + j * E;
+      if constexpr (CACHE) copy[it] = third;
       lo[it] = load_pack<T, E, true>(src);
       if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
     }
@@ -168,7 +141,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   for (int it = 0; it < ITERS; ++it) {
     if (dst[it] == nullptr) continue;
     if constexpr (CACHE) {
-      if (w.which == 2) {
+      if (copy[it]) {
         store_pack<T, E, true>(dst[it], lo[it]);
         if constexpr (NEOX) store_pack<T, E, true>(dst[it] + half, hi[it]);
         continue;
@@ -250,20 +223,12 @@ RopeTensorDev to_dev(const RopeTensorArgs& t) {
 }
 
 constexpr int kWavesPerBlock = 4;
-
-// Chunks per token, tensor by tensor, so that no wavefront spans two tensors.
-template <bool CACHE>
-void set_chunks(RopeDev& d, int64_t heads_per_chunk) {
-  d.chunks0 = static_cast<int>(ceil_div(d.t0.heads, heads_per_chunk));
-  d.chunks1 = static_cast<int>(ceil_div(d.t1.heads, heads_per_chunk));
-  d.chunks = d.chunks0 + d.chunks1 + (CACHE ? static_cast<int>(ceil_div(d.t2.heads, heads_per_chunk)) : 0);
-}
 constexpr int64_t kWavesPerLaunch = int64_t(1) << 24;  // keeps grid work-items < 2^32
 
 template <typename T, typename TT, bool NEOX, int ITERS, bool CACHE, int TPB = kWavesPerBlock>
 hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   const int64_t heads_per_wave = ITERS * (kWave / per_unit);
-  set_chunks<CACHE>(d, heads_per_wave);
+  d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads + (CACHE ? d.t2.heads : 0), heads_per_wave));
   d.pu_shift = (per_unit & (per_unit - 1)) == 0 ? __builtin_ctzll(per_unit) : -1;
   const int64_t tokens_per_launch = std::max<int64_t>(1, kWavesPerLaunch / d.chunks);
   for (int64_t first = 0; first < d.total_tokens; first += tokens_per_launch) {
@@ -316,7 +281,7 @@ hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
 
 template <typename T, typename TT>
 hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
-  RopeDev d{to_dev(a.t0), to_dev(a.t1), to_dev(a.t2), a.pos, a.cache_len, a.cos, a.sin, 0, 0, 1, 1, 0,
+  RopeDev d{to_dev(a.t0), to_dev(a.t1), to_dev(a.t2), a.pos, a.cache_len, a.cos, a.sin, 0, 0, 1,
             static_cast<int>(a.seq), static_cast<int>(a.head_dim), -1, a.st, a.batch * a.seq};
   if (a.vector_ok) {
     constexpr int E = 16 / sizeof(T);
