@@ -215,7 +215,7 @@ def main() -> int:
                 cells.append((f"rmsnorm_shard_partial_{tag}_{rows_tp}x{shard}_residual", nb_p,
                               lambda x=xs_tp[i], r=rs_tp[i]: rmsnorm_shard_partial_hip(x, r)))
                 cells.append((f"rmsnorm_shard_apply_{tag}_{rows_tp}x{shard}", nb_a,
-                              lambda s_=xs_tp[i]: rmsnorm_shard_apply_hip(s_, w_tp, tot, 8 * shard, 1e-6)))
+                              lambda s_=xs_tp[i], w_=w_tp, t_=tot: rmsnorm_shard_apply_hip(s_, w_, t_, 8 * shard, 1e-6)))
         for m in (16384, 4096, 256, 16, 1):
             dtype = torch.bfloat16
             nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)
