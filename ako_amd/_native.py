@@ -40,6 +40,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "ako_hip_runtime_version": (_int, []),
     "ako_build_info": (ctypes.c_char_p, []),
     "ako_last_error": (ctypes.c_char_p, []),
+    "ako_device_identity": (_int, [_int, ctypes.c_char_p, _i64]),
     "ako_rmsnorm_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _f32, _int, _int, _ptr]),
     "ako_rmsnorm_residual_fwd": (
         _int,
@@ -203,3 +204,14 @@ def set_tuning(op: int, key: int, value: int) -> None:
 def current_stream(device: torch.device) -> int:
     """Raw ``hipStream_t`` of torch's current stream on ``device``."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def device_identity(index: int) -> dict[str, str]:
+    """HIP's identity fields of GPU ``index`` (``ako_device_identity``) as a dict."""
+    buf = ctypes.create_string_buffer(1024)
+    check(load().ako_device_identity(int(index), buf, len(buf)), "ako_device_identity")
+    fields = {}
+    for item in buf.value.decode(errors="replace").split(";"):
+        key, _, value = item.partition("=")
+        fields[key] = value
+    return fields

@@ -110,6 +110,25 @@ const char* ako_build_info(void) {
 
 const char* ako_last_error(void) { return g_last_error.c_str(); }
 
+int ako_device_identity(int device, char* buf, int64_t buf_len) {
+  const char* fn = "ako_device_identity";
+  if (buf == nullptr || buf_len <= 0) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: no output buffer", fn);
+  hipDeviceProp_t props;
+  const hipError_t err = hipGetDeviceProperties(&props, device);
+  if (err != hipSuccess) return hip_status(err, fn);
+  int driver = 0;
+  if (hipDriverGetVersion(&driver) != hipSuccess) driver = -1;
+  props.name[sizeof(props.name) - 1] = '\0';
+  props.gcnArchName[sizeof(props.gcnArchName) - 1] = '\0';
+  const int n = std::snprintf(buf, static_cast<size_t>(buf_len),
+                              "name=%s;arch=%s;cus=%d;clock_khz=%d;mem_bytes=%llu;hip_driver=%d", props.name,
+                              props.gcnArchName, props.multiProcessorCount, props.clockRate,
+                              static_cast<unsigned long long>(props.totalGlobalMem), driver);
+  if (n < 0 || n >= buf_len) return fail(AKO_ERR_INVALID_ARGUMENT, "%s: buffer of %lld bytes is too small", fn,
+                                         static_cast<long long>(buf_len));
+  return AKO_OK;
+}
+
 int ako_set_tuning(int op, int key, int value) {
   if (value < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "tuning value must be >= 0, got %d", value);
   switch (op) {

@@ -92,16 +92,26 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
 
   const int b = token / a.seq;
   const int s = token - b * a.seq;
-  // Row of the tables and, in KV-cache mode, the cache slot of this token.
+  // Row of the tables and, in KV-cache mode, the cache slot of this token. A
+  // token whose slot falls outside the cache writes no cache slot, and its q
+  // rows are filled with NaN (table row 0 is read and replaced by NaN, so the
+  // rotation yields NaN): the broken contract shows instead of stale memory.
   int p = s;
+  [[maybe_unused]] bool dropped = false;
   if constexpr (CACHE) {
     const int64_t pp = *a.pos + s;
-    if (pp < 0 || pp >= a.cache_len) return;  // out of the cache: nothing is written
-    p = static_cast<int>(pp);
+    dropped = pp < 0 || pp >= a.cache_len;
+    p = dropped ? 0 : static_cast<int>(pp);
   }
   float c[NT], n[NT];
   load_f32<TT, NT>(static_cast<const TT*>(a.cos) + p * a.st + j * NT, c);
   load_f32<TT, NT>(static_cast<const TT*>(a.sin) + p * a.st + j * NT, n);
+  if constexpr (CACHE) {
+    if (dropped) {
+#pragma unroll
+      for (int e = 0; e < NT; ++e) c[e] = n[e] = __builtin_nanf("");
+    }
+  }
 
   const int h01 = static_cast<int>(a.t0.heads + a.t1.heads);
   const int total = h01 + (CACHE ? static_cast<int>(a.t2.heads) : 0);
@@ -113,7 +123,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   for (int it = 0; it < ITERS; ++it) {
     const int h = base + it * heads_per_iter + hl;
     dst[it] = nullptr;
-    if (h < total) {
+    if (h < total && !(CACHE && dropped && h >= a.t0.heads)) {
       const bool first = h < a.t0.heads;
       const bool third = CACHE && h >= h01;
       // The tensor is chosen field by field, by value: the fields then come
@@ -189,9 +199,11 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
     const int64_t b = token / a.seq;
     const int64_t s = token - b * a.seq;
     const int64_t p = CACHE ? p0 + s : s;
-    if (CACHE && (p < 0 || p >= a.cache_len)) continue;
     const bool first = h < a.t0.heads;
     const bool third = CACHE && h >= h01;
+    // Outside the cache: no cache slot is written and q gets NaN (as rope_vec).
+    const bool dropped = CACHE && (p < 0 || p >= a.cache_len);
+    if (dropped && !first) continue;
     // Field by field, by value (scalar loads and a select; see rope_vec).
     const auto pick = [&](const auto& f0, const auto& f1, const auto& f2) { return first ? f0 : (third ? f2 : f1); };
     const int64_t hh = first ? h : (third ? h - h01 : h - a.t0.heads);
@@ -205,6 +217,10 @@ __global__ __launch_bounds__(256) void rope_scalar(RopeDev a) {
     if (third) {
       dst[ia] = src[ia];
       dst[ib] = src[ib];
+      continue;
+    }
+    if (dropped) {
+      dst[ia] = dst[ib] = from_f32<T>(__builtin_nanf(""));
       continue;
     }
     const float c = to_f32(static_cast<const TT*>(a.cos)[p * a.st + i]);

@@ -86,20 +86,36 @@ int on_device(int index, F&& launch) {
   return launch(at::hip::getCurrentHIPStream(index).stream());
 }
 
+// Stride between consecutive rows of the last dimension when the leading dims
+// can be walked as one run of equally spaced rows, else -1. Size-1 dims are
+// transparent (their stride is arbitrary and never multiplies an index); the
+// innermost leading dim of size > 1 fixes the row stride, and each outer one of
+// size > 1 must be that stride times the rows spanned by the dims inside it.
+int64_t leading_row_stride(const at::Tensor& t) {
+  const int64_t h = t.size(-1);
+  int64_t row_stride = -1, spanned = 1;
+  for (int64_t i = t.dim() - 2; i >= 0; --i) {
+    if (t.size(i) == 1) continue;
+    if (row_stride < 0) {
+      row_stride = t.stride(i);
+      spanned = t.size(i);
+    } else if (t.stride(i) != row_stride * spanned) {
+      return -1;
+    } else {
+      spanned *= t.size(i);
+    }
+  }
+  if (row_stride < 0) return h;
+  return row_stride >= h ? row_stride : -1;
+}
+
 // (tensor, row stride): rows of the last dimension at r * row_stride, copying
 // only when the leading dims cannot be walked with one stride.
 std::pair<at::Tensor, int64_t> rows_view(const at::Tensor& t) {
   if (t.is_contiguous()) return {t, t.dim() ? t.size(-1) : 1};
-  if (t.dim() >= 2 && t.stride(-1) == 1) {
-    const int64_t row_stride = t.stride(-2);
-    bool ok = true;
-    for (int64_t i = 0; i + 2 < t.dim(); ++i) {
-      if (t.size(i) != 1 && t.stride(i) != t.stride(i + 1) * t.size(i + 1)) {
-        ok = false;
-        break;
-      }
-    }
-    if (ok && (t.size(-2) == 1 || row_stride >= t.size(-1))) return {t, row_stride};
+  if (t.dim() >= 2 && (t.stride(-1) == 1 || t.size(-1) <= 1)) {
+    const int64_t row_stride = leading_row_stride(t);
+    if (row_stride >= 0) return {t, row_stride};
   }
   at::Tensor c = t.contiguous();
   return {c, c.size(-1)};
@@ -333,6 +349,12 @@ int64_t current_stream(int64_t index) {
   return reinterpret_cast<int64_t>(at::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(index)).stream());
 }
 
+// The row walk rows_view takes for t, for host tests: (copied, row stride).
+std::pair<bool, int64_t> row_walk(const at::Tensor& t) {
+  auto [v, stride] = rows_view(t);
+  return {!v.is_same(t), stride};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_ako_torch, m) {
@@ -348,4 +370,5 @@ PYBIND11_MODULE(_ako_torch, m) {
         py::arg("sin"), py::arg("pos"), py::arg("k_cache"), py::arg("v_cache"), py::arg("style") = "neox");
   m.def("swiglu", &swiglu, py::arg("gate"), py::arg("up"));
   m.def("current_stream", &current_stream);
+  m.def("row_walk", &row_walk, py::arg("t"));
 }

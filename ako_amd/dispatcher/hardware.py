@@ -3,11 +3,21 @@
 Replaces ``ako/dispatcher/hardware.py:22-193`` of the reference, which read
 CUDA attributes through ``ctypes.CDLL("libcudart.so")`` and the driver through
 ``nvidia-smi``. Here everything comes from the HIP runtime that PyTorch-ROCm
-already initialised (``torch.cuda.get_device_properties`` is a thin wrapper of
-``hipGetDeviceProperties``) plus the amdgpu kernel module's version file, so
-no subprocess runs on the dispatch path. The ``DeviceInfo`` fields and the
-``cache_key`` format (``"<name with _ for spaces>_<index>"``) are the
-reference's, so cache files stay keyed the same way.
+already initialised: ``hipGetDeviceProperties`` and ``hipDriverGetVersion``
+through the library's ``ako_device_identity``, or torch's property object when
+the library is not loaded. No subprocess runs on the dispatch path. The
+``DeviceInfo`` fields and the ``cache_key`` format
+(``"<name with _ for spaces>_<index>"``) are the reference's, so cache files
+stay keyed the same way.
+
+The reference keys selections by the product name (``hardware.py:60-63``). On
+ROCm the name HIP reports can be the generic "AMD Radeon Graphics" for every
+part, so ``device_name`` here is that name followed by the fields that tell
+parts apart: the ISA, the compute-unit count, the peak engine clock and the
+HBM size (``"AMD Radeon Graphics gfx950 256CU 2400MHz 288GB"``). An MI300X
+(gfx942, 304 CUs) and an MI355X (gfx950, 256 CUs, 2400 MHz) never share a key,
+nor do an MI350X and an MI355X (the same ISA and CU count, 2200 against
+2400 MHz).
 """
 
 from __future__ import annotations
@@ -40,6 +50,10 @@ class DeviceInfo:
     #: ``gcnArchName`` with feature flags, e.g. ``gfx950:sramecc+:xnack-``.
     gcn_arch: str | None = None
     hip_runtime: str | None = None
+    #: The name exactly as HIP reports it (``device_name`` adds the part fields).
+    marketing_name: str | None = None
+    #: Peak engine clock in MHz (``hipDeviceProp_t.clockRate``).
+    clock_mhz: int | None = None
 
     @property
     def cache_key(self) -> str:
@@ -62,13 +76,57 @@ def _compute_backend() -> str:
 
 
 @lru_cache(maxsize=1)
-def _amdgpu_driver_version() -> str | None:
-    """The amdgpu kernel-module version, read from sysfs (no subprocess)."""
+def _amdgpu_module_version() -> str | None:
+    """The amdgpu kernel-module version from sysfs, where the module has one
+    (a DKMS build does; the in-tree module of many kernels does not)."""
     try:
         text = Path("/sys/module/amdgpu/version").read_text().strip()
     except OSError:
         return None
     return text or None
+
+
+def driver_label(module_version: str | None, hip_driver: int | None) -> str | None:
+    """``"amdgpu <version>"`` when the module reports one, else the HIP driver
+    version (``hipDriverGetVersion``, which every ROCm install answers)."""
+    if module_version:
+        return f"amdgpu {module_version}"
+    if hip_driver is not None and hip_driver > 0:
+        return f"hip {hip_driver}"
+    return None
+
+
+def part_label(name: str, arch: str | None, cus: int | None, clock_khz: int | None,
+               mem_bytes: int | None) -> str:
+    """HIP's device name followed by the fields that tell parts apart:
+    ``"<name> <isa> <cus>CU <MHz>MHz <GiB>GB"``; missing fields are left out."""
+    parts = [name.strip() or "AMD GPU"]
+    if arch:
+        parts.append(arch.split(":")[0])
+    if cus:
+        parts.append(f"{int(cus)}CU")
+    if clock_khz and clock_khz > 0:
+        parts.append(f"{int(round(clock_khz / 1000))}MHz")
+    if mem_bytes and mem_bytes > 0:
+        parts.append(f"{int(round(mem_bytes / 1024**3))}GB")
+    return " ".join(parts)
+
+
+def _hip_identity(index: int) -> dict[str, str] | None:
+    """``ako_device_identity`` fields, or None when the library is not usable."""
+    try:
+        from ako_amd import _native
+
+        return _native.device_identity(index)
+    except Exception:  # noqa: BLE001 - a missing library falls back to torch's props
+        return None
+
+
+def _int_or_none(text: str | None) -> int | None:
+    try:
+        return int(text) if text not in (None, "") else None
+    except ValueError:
+        return None
 
 
 def get_device_info(device: torch.device | str | None = None) -> DeviceInfo:
@@ -91,21 +149,32 @@ def clear_device_cache() -> None:
     """Forget memoised probes (tests)."""
     _device_info.cache_clear()
     _compute_backend.cache_clear()
-    _amdgpu_driver_version.cache_clear()
+    _amdgpu_module_version.cache_clear()
 
 
 @lru_cache(maxsize=None)
 def _device_info(device_type: str, device_index: int | None) -> DeviceInfo:
     backend = _compute_backend()
     if device_type == "cuda" and torch.cuda.is_available():
-        props = torch.cuda.get_device_properties(device_index or 0)
+        index = device_index or 0
+        props = torch.cuda.get_device_properties(index)
+        ident = _hip_identity(index) if backend == "rocm" else None
+        ident = ident or {}
+        arch = ident.get("arch") or getattr(props, "gcnArchName", None)
+        cus = _int_or_none(ident.get("cus")) or getattr(props, "multi_processor_count", None)
+        clock_khz = _int_or_none(ident.get("clock_khz"))
+        mem_bytes = _int_or_none(ident.get("mem_bytes")) or props.total_memory
+        raw_name = ident.get("name") or props.name
+        name = part_label(raw_name, arch, cus, clock_khz, mem_bytes) if backend == "rocm" else props.name
+        driver = (driver_label(_amdgpu_module_version(), _int_or_none(ident.get("hip_driver")))
+                  if backend == "rocm" else None)
         return DeviceInfo(
             device_type="cuda",
-            device_name=props.name,
-            device_index=device_index or 0,
+            device_name=name,
+            device_index=index,
             cuda_capability=(props.major, props.minor),
             total_memory_gb=round(props.total_memory / 1024**3, 2),
-            driver_version=_amdgpu_driver_version() if backend == "rocm" else None,
+            driver_version=driver,
             gpu_vendor="amd" if backend == "rocm" else "nvidia",
             compute_backend=backend,
             sm_count=getattr(props, "multi_processor_count", None),
@@ -115,8 +184,10 @@ def _device_info(device_type: str, device_index: int | None) -> DeviceInfo:
             ),
             l2_bytes=getattr(props, "L2_cache_size", None),
             regs_per_sm=getattr(props, "regs_per_multiprocessor", None),
-            gcn_arch=getattr(props, "gcnArchName", None),
+            gcn_arch=arch,
             hip_runtime=getattr(torch.version, "hip", None),
+            marketing_name=raw_name,
+            clock_mhz=int(round(clock_khz / 1000)) if clock_khz else None,
         )
     return DeviceInfo(
         device_type=device_type,

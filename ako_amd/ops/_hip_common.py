@@ -61,20 +61,42 @@ def call(index: int, fn, *args) -> int:
         return fn(*args)
 
 
+def leading_row_stride(shape, strides) -> int | None:
+    """Stride between consecutive rows of the last dimension when the leading
+    dims (all but the last) can be walked as one run of equally spaced rows,
+    else ``None``.
+
+    Size-1 dims are transparent: their stride is arbitrary in torch and never
+    multiplies an index. The innermost leading dim of size > 1 fixes the row
+    stride; every outer one of size > 1 must then be that stride times the
+    number of rows the dims inside it span. With at most one row the stride
+    is the row length (it is never used to step)."""
+    h = shape[-1] if len(shape) else 1
+    row_stride = None
+    spanned = 1
+    for size, stride in zip(reversed(shape[:-1]), reversed(strides[:-1])):
+        if size == 1:
+            continue
+        if row_stride is None:
+            row_stride, spanned = stride, size
+        elif stride != row_stride * spanned:
+            return None
+        else:
+            spanned *= size
+    if row_stride is None:
+        return h
+    return row_stride if row_stride >= h else None
+
+
 def rows_view(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     """``(tensor, row_stride)`` such that row r of the last dimension starts at
     ``r * row_stride``; copies only when the leading dims cannot be walked with
     one stride or the last dimension is not contiguous."""
     if t.is_contiguous():
         return t, t.shape[-1] if t.dim() else 1
-    if t.dim() >= 2 and t.stride(-1) == 1:
-        row_stride = t.stride(-2)
-        ok = True
-        for i in range(t.dim() - 2):
-            if t.shape[i] != 1 and t.stride(i) != t.stride(i + 1) * t.shape[i + 1]:
-                ok = False
-                break
-        if ok and (t.shape[-2] == 1 or row_stride >= t.shape[-1]):
+    if t.dim() >= 2 and (t.stride(-1) == 1 or t.shape[-1] <= 1):
+        row_stride = leading_row_stride(t.shape, t.stride())
+        if row_stride is not None:
             return t, row_stride
     t = t.contiguous()
     return t, t.shape[-1]

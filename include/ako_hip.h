@@ -64,6 +64,18 @@ const char* ako_build_info(void);
 const char* ako_last_error(void);
 
 /*
+ * Identity of GPU `device` for the selection cache key, written into buf as
+ * one NUL-terminated line of key=value fields separated by ';':
+ *   name=<hipDeviceProp_t.name>;arch=<gcnArchName>;cus=<CUs>;
+ *   clock_khz=<peak engine clock>;mem_bytes=<HBM bytes>;hip_driver=<hipDriverGetVersion>
+ * Replaces the device-name probe of ako/dispatcher/hardware.py:134-193 (CUDA
+ * runtime attributes and nvidia-smi). The marketing name that HIP reports can
+ * be a generic "AMD Radeon Graphics" for every part, so callers key by the
+ * other fields too. Returns AKO_ERR_INVALID_ARGUMENT when buf is too small.
+ */
+int ako_device_identity(int device, char* buf, int64_t buf_len);
+
+/*
  * RMSNorm over the last dimension:
  *   y[r, :] = to_dtype( (x[r, :] * rsqrt(sum(x[r, :]^2) / hidden + eps)) * w[:] )
  * x, y: dtype; w: w_dtype (== dtype, or AKO_DTYPE_F32).
@@ -161,9 +173,11 @@ int ako_rope_qk_fwd(const void* q, const void* k, const void* cos_table, const v
  *   v_cache[b, h, slot p] = v[b, s, h]          (v and v_cache may both be NULL)
  * q/k/v/q_out strides are (batch, seq, head); cache_strides (batch, slot,
  * head) are shared by both caches, in elements. The tables hold table_rows
- * >= cache_len rows. Tokens whose p falls outside [0, cache_len) are not
- * written at all (q_out included); keeping *pos + seq <= cache_len is the
- * caller's contract, as it is for the reference's cache.
+ * >= cache_len rows. A token whose p falls outside [0, cache_len) writes no
+ * cache slot, and its q_out rows are filled with NaN; keeping
+ * *pos + seq <= cache_len is the caller's contract (the reference's unfused
+ * composition raises an index error there, which a position held in device
+ * memory cannot do).
  */
 int ako_rope_qk_cache_fwd(const void* q, const void* k, const void* v,
                           const void* cos_table, const void* sin_table,

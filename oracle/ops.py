@@ -166,13 +166,14 @@ def rope_qk_cache(q: np.ndarray, k: np.ndarray, v: np.ndarray | None, cos: np.nd
     ``(positions, head_dim/2)`` ones, read at the same rows.
 
     Returns ``(q_rotated, new_k_cache, new_v_cache)``; the inputs are not
-    modified. Tokens whose slot falls outside the cache are dropped (q rows
-    included, which are returned as zeros), matching the kernel contract.
+    modified. Tokens whose slot falls outside the cache write no slot, and
+    their q rows are NaN: the library's contract where the reference's
+    ``index_select`` would raise (a position in device memory cannot raise).
     """
     seq = q.shape[1]
     cache_len = k_cache.shape[2]
     keep = [s for s in range(seq) if 0 <= pos + s < cache_len]
-    q_out = np.zeros_like(q)
+    q_out = round_to(np.full(q.shape, np.nan, np.float32), dtype)
     new_k = k_cache.copy()
     new_v = None if v_cache is None else v_cache.copy()
     if not keep:

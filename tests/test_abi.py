@@ -22,6 +22,14 @@ OK, INVALID, UNSUPPORTED = 0, 1, 2
 F32, F16, BF16 = 0, 1, 2
 A, B, C, D, E = 0x100000, 0x200000, 0x300000, 0x400000, 0x500000
 
+# Tests that hand the entry points the fake addresses above rely on the
+# validation layer refusing the call before any launch. Where a GPU is
+# visible a regression there would launch a kernel on those addresses, so
+# they run only where no GPU can be launched on (the CPU suite).
+fake_addresses = pytest.mark.skipif(
+    torch.cuda.is_available(),
+    reason="passes fake device addresses: runs only where no GPU is visible")
+
 
 @pytest.fixture(scope="module")
 def lib():
@@ -60,6 +68,7 @@ def rms(lib, **kw):
                                args["sx"], args["sy"], args["eps"], args["dt"], args["wdt"], None)
 
 
+@fake_addresses
 def test_rmsnorm_validation(lib) -> None:
     assert rms(lib, rows=0) == OK
     assert rms(lib, hidden=0) == OK
@@ -77,6 +86,7 @@ def test_rmsnorm_validation(lib) -> None:
     assert rms(lib, sx=-64) == INVALID
 
 
+@fake_addresses
 def test_rmsnorm_residual_validation(lib) -> None:
     f = lib.ako_rmsnorm_residual_fwd
     base = [A, B, E, C, D, 4, 64, 64, 64, 64, 64, 1e-6, BF16, F32, None]
@@ -97,6 +107,7 @@ def rope(lib, **kw):
                             *a["xs"], *a["ys"], a["st"], a["dt"], a["tdt"], a["style"], None)
 
 
+@fake_addresses
 def test_rope_validation(lib) -> None:
     assert rope(lib, b=0) == OK
     assert rope(lib, h=0) == OK
@@ -110,6 +121,7 @@ def test_rope_validation(lib) -> None:
     assert rope(lib, st=2) == INVALID  # table rows shorter than head_dim/2
 
 
+@fake_addresses
 def test_rope_qk_validation(lib) -> None:
     s = (ctypes.c_int64 * 3)(64, 16, 8)
     f = lib.ako_rope_qk_fwd
@@ -119,6 +131,7 @@ def test_rope_qk_validation(lib) -> None:
     assert f(A, None, C, D, E, 0x600000, 1, 4, 2, 2, 8, s, s, s, s, 4, F16, F32, 0, None) == INVALID
 
 
+@fake_addresses
 def test_rope_qk_cache_validation(lib) -> None:
     """KV-cache RoPE: argument checks that run before any launch."""
     f = lib.ako_rope_qk_cache_fwd
@@ -142,6 +155,7 @@ def test_rope_qk_cache_validation(lib) -> None:
     assert call(kc=COS) == INVALID and "table" in _native.last_error()
 
 
+@fake_addresses
 def test_swiglu_validation(lib) -> None:
     f = lib.ako_swiglu_fwd
     assert f(A, B, C, 0, 16, 16, 16, 16, BF16, None) == OK
@@ -152,6 +166,7 @@ def test_swiglu_validation(lib) -> None:
     assert f(None, B, C, 4, 16, 16, 16, 16, BF16, None) == INVALID
 
 
+@fake_addresses
 def test_sizes_that_overflow_the_address_space_are_rejected(lib) -> None:
     """Extents are computed in 128 bits: huge sizes or strides cannot wrap into
     a small span that would pass the overlap checks."""

@@ -193,6 +193,65 @@ def test_device_info_cpu() -> None:
     assert (info.device_type, info.compute_backend, info.cache_key) == ("cpu", "cpu", "cpu_-1")
 
 
+# HIP's answers for three parts that all report the generic marketing name:
+# (gcnArchName, CUs, peak engine clock kHz, HBM bytes).
+_PARTS = {
+    "mi300x": ("gfx942:sramecc+:xnack-", 304, 2_100_000, 192 * 1024**3),
+    "mi350x": ("gfx950:sramecc+:xnack-", 256, 2_200_000, 288 * 1024**3),
+    "mi355x": ("gfx950:sramecc+:xnack-", 256, 2_400_000, 288 * 1024**3),
+}
+
+
+def _fake_rocm_device(monkeypatch, part: str, *, library: bool = True):
+    from functools import lru_cache
+    from types import SimpleNamespace
+
+    from ako_amd.dispatcher import hardware
+
+    arch, cus, clock, mem = _PARTS[part]
+    props = SimpleNamespace(name="AMD Radeon Graphics", major=9, minor=5, total_memory=mem,
+                            multi_processor_count=cus, gcnArchName=arch, L2_cache_size=4 << 20,
+                            regs_per_multiprocessor=524288, shared_memory_per_block=65536)
+    ident = {"name": "AMD Radeon Graphics", "arch": arch, "cus": str(cus), "clock_khz": str(clock),
+             "mem_bytes": str(mem), "hip_driver": "70226015"}
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda i: props)
+    monkeypatch.setattr(torch.version, "hip", "7.0.51831", raising=False)
+    monkeypatch.setattr(hardware, "_hip_identity", lambda i: ident if library else None)
+    monkeypatch.setattr(hardware, "_amdgpu_module_version", lru_cache(maxsize=1)(lambda: None))
+    hardware.clear_device_cache()
+    return hardware
+
+
+def test_cache_key_tells_amd_parts_apart(monkeypatch) -> None:
+    """The generic HIP name alone would give every part the same key; the ISA,
+    CU count, clock and HBM size make each part's key its own."""
+    keys = {}
+    for part in _PARTS:
+        hardware = _fake_rocm_device(monkeypatch, part)
+        info = hardware.get_device_info("cuda:0")
+        keys[part] = info.cache_key
+        assert info.marketing_name == "AMD Radeon Graphics"
+        assert info.driver_version == "hip 70226015"
+    assert keys["mi355x"] == "AMD_Radeon_Graphics_gfx950_256CU_2400MHz_288GB_0"
+    assert keys["mi300x"] == "AMD_Radeon_Graphics_gfx942_304CU_2100MHz_192GB_0"
+    assert len(set(keys.values())) == 3
+    # Without the library (torch's properties only): no clock, still the ISA.
+    hardware = _fake_rocm_device(monkeypatch, "mi300x", library=False)
+    assert hardware.get_device_info("cuda:0").cache_key == "AMD_Radeon_Graphics_gfx942_304CU_192GB_0"
+    hardware.clear_device_cache()
+
+
+def test_driver_label_prefers_the_module_version() -> None:
+    from ako_amd.dispatcher.hardware import driver_label, part_label
+
+    assert driver_label("6.10.5", 70226015) == "amdgpu 6.10.5"
+    assert driver_label(None, 70226015) == "hip 70226015"
+    assert driver_label(None, None) is None
+    assert part_label("AMD Instinct MI355X", "gfx950:xnack-", 256, 2_400_000, None) == \
+        "AMD Instinct MI355X gfx950 256CU 2400MHz"
+
+
 def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
     """The reset/clear helpers the reference exposes for tests, and
     ``load_baseline`` for its regression diffs, behave as their names say."""

@@ -38,6 +38,20 @@ def test_selector_picks_hip_and_records_it(tmp_path) -> None:
     assert again.source == "cache" and again.entry.kernel_name == "rmsnorm_hip"
 
 
+def test_cache_key_names_the_part() -> None:
+    """The selection cache key carries the ISA and CU count that HIP reports,
+    and a driver version (never null on a ROCm box)."""
+    from ako_amd.dispatcher.hardware import clear_device_cache, get_device_info
+
+    clear_device_cache()
+    info = get_device_info("cuda:0")
+    print(f"device_name={info.device_name!r} cache_key={info.cache_key!r} driver={info.driver_version!r}")
+    assert "gfx950" in info.cache_key and f"{info.sm_count}CU" in info.cache_key
+    assert info.cache_key.endswith("_0") and " " not in info.cache_key
+    assert info.clock_mhz and info.clock_mhz > 500
+    assert info.driver_version
+
+
 def test_public_api_on_gpu_passes_the_gate() -> None:
     x = _rand(4, 256, 4096, dtype=torch.float16)
     r = _rand(4, 256, 4096, dtype=torch.float16, seed=2)

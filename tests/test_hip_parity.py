@@ -15,6 +15,8 @@ Every case checks two things on identical seeded inputs:
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -242,6 +244,64 @@ def test_rmsnorm_empty_and_errors() -> None:
 ROPE_BS = [(1, 1), (64, 1), (4, 2048)]
 
 
+def _half_ulp_distance(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """Distance in ulps between two arrays of 16-bit float patterns."""
+    def ordered(bits):
+        b = bits.astype(np.int32)
+        return np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + b)
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+@pytest.mark.parametrize("seq", [1, 640, 2048])
+def test_device_built_tables_match_the_oracle(seq: int) -> None:
+    """``build_rope_tables(device="cuda")`` against ``oracle.rope_tables``.
+
+    fp32: the GPU's ``pow`` (inv_freq) and ``cos``/``sin`` are 1-2 ulp
+    functions, and an inv_freq 1 ulp off moves the angle ``pos * inv_freq`` by
+    about ``|angle| * 2^-23``, which the table value inherits in absolute
+    terms. The bound is therefore 2 ulp of 1 plus 3 angle ulps:
+    ``2 * 2^-24 + 3 * |angle| * 2^-23``. fp16/bf16 tables are the fp32 tables
+    narrowed on the device (bit for bit), and within one ulp of the oracle's
+    narrowed tables plus the same angle term.
+    """
+    d = 128
+    cos, sin = build_rope_tables(seq, d, device=DEV)
+    assert cos.dtype == torch.float32 and cos.shape == (seq, d // 2) and cos.is_cuda
+    ec, es = oracle.rope_tables(seq, d)
+    # The angles as the oracle forms them (fp32 rounded once per step).
+    half = d // 2
+    inv = np.float32(1.0) / np.power(np.float64(10000.0),
+                                     (np.arange(half, dtype=np.float32) * 2 / d).astype(np.float64)).astype(np.float32)
+    angles = np.abs(np.outer(np.arange(seq, dtype=np.float32), inv).astype(np.float64))
+    bound = 2 * 2.0**-24 + 3 * angles * 2.0**-23
+    for got, exp in ((cos, ec), (sin, es)):
+        diff = np.abs(got.cpu().numpy().astype(np.float64) - exp.astype(np.float64))
+        assert np.all(diff <= bound), (float(diff.max()), float((diff / bound).max()))
+    # Known values: position 0 is the identity, position 1 rotates pair 0 by 1 rad.
+    assert torch.all(cos[0] == 1.0) and torch.all(sin[0] == 0.0)
+    if seq > 1:
+        assert abs(float(cos[1, 0]) - math.cos(1.0)) <= 2 * 2.0**-24
+        assert abs(float(sin[1, 0]) - math.sin(1.0)) <= 2 * 2.0**-24
+    # Offsets are a shift of the same tables (same fp32 operations per row).
+    if seq > 8:
+        oc, osn = build_rope_tables(8, d, offset=seq - 8, device=DEV)
+        assert torch.equal(oc, cos[-8:]) and torch.equal(osn, sin[-8:])
+    for dtype in (torch.float16, torch.bfloat16):
+        hc, hs = build_rope_tables(seq, d, device=DEV, dtype=dtype)
+        assert torch.equal(hc, cos.to(dtype)) and torch.equal(hs, sin.to(dtype))
+        name = NAMES[dtype]
+        unit = {torch.float16: 2.0**-11, torch.bfloat16: 2.0**-8}[dtype]
+        for got, exp32 in ((hc, ec), (hs, es)):
+            exp = oracle.round_to(exp32, name)
+            g, e = to_np(got), exp
+            close = _half_ulp_distance(g.view(np.uint16), e.view(np.uint16)) <= 1
+            # Where the fp32 values straddle a rounding boundary by more than
+            # the angle term, one more ulp is allowed.
+            near = np.abs(got.float().cpu().numpy().astype(np.float64) - exp32.astype(np.float64)) <= \
+                unit + bound
+            assert np.all(close | near)
+
+
 @pytest.mark.parametrize("style", ["neox", "interleaved"])
 @pytest.mark.parametrize("table_dtype", ["x", torch.float32])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -323,9 +383,12 @@ def test_rope_qk_cache(batch, seq, hq, hkv, d, pos, cache_len, style: str, dtype
                                       to_np(kc), to_np(vc), style, dtype=NAMES[dtype])
     q_out = rope_qk_cache_hip(q, k, v, cos, sin, pos_t, kc, vc, style)
     kept = [s for s in range(seq) if pos + s < cache_len]
+    dropped = [s for s in range(seq) if pos + s >= cache_len]
     untouched = [t for t in range(cache_len) if not pos <= t < pos + len(kept)]
     # RoPE rounds the oracle's own fp32 products and sums: bit for bit.
     np.testing.assert_array_equal(to_np(q_out[:, kept]), eq[:, kept])
+    # Tokens past the cache: every q element NaN (never stale memory).
+    assert torch.isnan(q_out[:, dropped].float()).all()
     np.testing.assert_array_equal(to_np(kc), ek)
     np.testing.assert_array_equal(to_np(vc), ev)
     # The same rotation as the one-launch pair kernel on the same table rows, bit for bit.
@@ -415,6 +478,49 @@ def test_swiglu_extremes_and_strides(dtype) -> None:
     assert_oracle(oracle.swiglu(to_np(gm), to_np(um), dtype=NAMES[dtype]), to_np(swiglu_hip(gm, um)), dtype)
     empty = torch.empty(0, 14336, device=DEV, dtype=dtype)
     assert swiglu_hip(empty, empty).shape == (0, 14336)
+
+
+@pytest.mark.parametrize("binding", ["cpp", "ctypes"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_views_with_size1_leading_dims(dtype, binding) -> None:
+    """4-D views whose leading dims cannot be walked with one row stride
+    (a size-1 dim in front of a sliced one: rows 0..3 are 256 elements apart,
+    row 4 is 2048 further) and views that can (a size-1 row dim whose rows
+    sit at the outer stride). Each must give the contiguous input's result."""
+    from ako_amd import _native
+    from ako_amd.ops import rmsnorm_hip as rm
+    from ako_amd.ops import swiglu_hip as sw
+
+    fast = _native.torch_binding()
+    if binding == "cpp":
+        if fast is None:
+            pytest.skip("the C++ binding is not built")
+        f_rms, f_res, f_sw = fast.rmsnorm, fast.rmsnorm_residual, fast.swiglu
+    else:
+        f_rms, f_res, f_sw = rm.rmsnorm_hip_ctypes, rm.rmsnorm_residual_hip_ctypes, sw.swiglu_hip_ctypes
+    h = 256
+    big_x = grandn((2, 1, 8, h), dtype, 40)
+    big_r = grandn((2, 1, 8, h), dtype, 41)
+    w = grandn((h,), dtype, 42, scale=0.1, shift=1.0)
+    views = [
+        (big_x[:, :, :4, :], big_r[:, :, :4, :]),
+        (big_x[:, :, 2:3, :], big_r[:, :, 5:6, :]),
+        (big_x.permute(2, 1, 0, 3)[:3], big_r.permute(2, 1, 0, 3)[:3]),
+    ]
+    for x, r in views:
+        xc, rc = x.contiguous(), r.contiguous()
+        ey = oracle.rmsnorm(to_np(xc), to_np(w), dtype=NAMES[dtype])
+        y = f_rms(x, w, 1e-6)
+        assert y.shape == x.shape
+        assert_oracle(ey, to_np(y), dtype)
+        assert torch.equal(y, f_rms(xc, w, 1e-6))
+        y2, s2 = f_res(x, r, w, 1e-6)
+        ey2, es2 = oracle.rmsnorm_residual(to_np(xc), to_np(rc), to_np(w), dtype=NAMES[dtype])
+        np.testing.assert_array_equal(to_np(s2), es2)
+        assert_oracle(ey2, to_np(y2), dtype)
+        g = f_sw(x, r)
+        assert_oracle(oracle.swiglu(to_np(xc), to_np(rc), dtype=NAMES[dtype]), to_np(g), dtype)
+        assert torch.equal(g, f_sw(xc, rc))
 
 
 def _ordered16(bits: np.ndarray) -> np.ndarray:

@@ -238,7 +238,9 @@ def test_rope_qk_cache_drops_out_of_range_tokens() -> None:
     cos, sin = ops.rope_tables(6, 8)
     q_out, new_k, new_v = ops.rope_qk_cache(q, k, None, cos, sin, 4, kc, None)
     assert new_v is None
-    assert np.any(q_out[:, :2]) and not np.any(q_out[:, 2:])   # slots 4, 5 kept; 6, 7 dropped
+    # slots 4, 5 kept; 6, 7 outside the cache: no slot written, q rows NaN
+    assert not np.isnan(q_out[:, :2]).any() and np.any(q_out[:, :2])
+    assert np.isnan(q_out[:, 2:]).all()
     assert np.any(new_k[:, :, 4:]) and not np.any(new_k[:, :, :4])
 
 

@@ -53,6 +53,8 @@ def test_reference_slices_compose_to_the_full_row(dtype: torch.dtype, shards: in
         rmsnorm_sharded(x, r, w, shards=3, **REFS)
 
 
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="passes fake device addresses: runs only where no GPU is visible")
 def test_shard_abi_validation() -> None:
     lib = _native.load()
     A, B, C, D = 0x100000, 0x200000, 0x300000, 0x400000
