@@ -249,3 +249,64 @@ def copy_same_bytes(alg_bytes: int, *, timeout_s: float = 120.0) -> dict[str, An
     if proc.returncode != 0:
         return None
     return parse_copy_ceiling(proc.stdout)
+
+
+def _capture(thunks: Sequence[Callable[[], Any]]) -> "torch.cuda.CUDAGraph":
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for fn in thunks:
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in thunks:
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def _time_replays(graph: "torch.cuda.CUDAGraph", replays: int) -> float:
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph.replay()
+    torch.cuda.synchronize()
+    begin.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) / replays
+
+
+def time_graph_cold(fns: Sequence[Callable[[], Any]], *, evict_bytes: int | None = None,
+                    replays: int = 4, rounds: int = 5) -> float:
+    """Device microseconds per call when every call finds its inputs in no cache.
+
+    ``fns`` are calls on independent input copies (up to 64 are used). One HIP
+    graph holds an eviction pass followed by one call of each; a second graph
+    holds the eviction pass alone. The eviction is an elementwise
+    read-modify-write (torch's ``add_``, a plain kernel: no memset is
+    recorded) of a buffer of twice the L2s plus the Infinity Cache, so after
+    it no input of the calls is cached anywhere. The cold cost per call is the
+    difference of the two graphs' replay times over the number of calls: the
+    median over ``rounds`` alternating measurements.
+    """
+    calls = list(fns)[:64]
+    if evict_bytes is None:
+        evict_bytes = 2 * CACHE_BYTES.get(device_arch() or "", CACHE_BYTES["gfx950"])
+    scratch = torch.zeros(max(1, evict_bytes // 4), dtype=torch.float32, device=torch.cuda.current_device())
+
+    def evict() -> None:
+        scratch.add_(1.0)
+
+    with_calls = _capture([evict, *calls])
+    alone = _capture([evict])
+    diffs = []
+    for _ in range(rounds):
+        t_both = _time_replays(with_calls, replays)
+        t_evict = _time_replays(alone, replays)
+        diffs.append((t_both - t_evict) * 1e3 / len(calls))
+    del with_calls, alone, scratch
+    return statistics.median(diffs)

@@ -18,7 +18,7 @@ import argparse
 import json
 import sys
 from pathlib import Path
-from typing import Any, Iterator
+from typing import Any, Callable, Iterator
 
 import torch
 
@@ -89,14 +89,30 @@ def cell_name(op: str, shape: list[int], dtype: torch.dtype) -> str:
     return f"{op}_{tag}_{'x'.join(map(str, shape))}"
 
 
+def is_decode(op: str, shape: list[int]) -> bool:
+    """Decode-sized cells: at most 32 rows, one token per sequence, M <= 16."""
+    if op in ("rmsnorm", "rmsnorm_residual"):
+        return shape[0] <= 32
+    if op in ("rope", "rope_qk"):
+        return shape[1] == 1
+    return shape[0] <= 16
+
+
 def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
-        counters: dict[str, Any] | None = None) -> dict[str, Any]:
+        counters: dict[str, Any] | None = None,
+        keep: Callable[[str, list[int], torch.dtype], bool] | None = None,
+        quiet: bool = False) -> dict[str, Any]:
+    """Select every cell (or those ``keep(op, shape, dtype)`` accepts); write
+    one report per op and a summary, and return the summary."""
     device = torch.device("cuda", torch.cuda.current_device())
     info = get_device_info(device)
     registry = register_all(KernelRegistry())
     reports: dict[str, BenchmarkReport] = {}
-    wins = total = 0
+    wins = total = decode_total = decode_wins = 0
+    others: list[dict[str, Any]] = []
     for op, shape, dtype, tensors, kw in cells(ops, device):
+        if keep is not None and not keep(op, shape, dtype):
+            continue
         selector = KernelSelector(registry=registry, cache=KernelCache(path=out_dir / "sweep_cache.json"),
                                   auto_tune=True, warmup=warmup, repeats=repeats)
         result = selector.select_entry(op, *tensors, **kw)
@@ -120,10 +136,18 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
             latencies_ms={k: round(v, 5) for k, v in lat.items()},
             rejected=list(result.rejected),
         )
+        hip_won = result.entry.backend == "hip"
         total += 1
-        wins += int(result.entry.backend == "hip")
-        print(f"[sweep] {op:17s} {str(shape):22s} {str(dtype)[6:]:9s} -> {result.entry.kernel_name:22s} "
-              + " ".join(f"{k}={v * 1e3:.1f}us" for k, v in lat.items()), flush=True)
+        wins += int(hip_won)
+        if is_decode(op, shape):
+            decode_total += 1
+            decode_wins += int(hip_won)
+        if not hip_won:
+            others.append({"cell": cell_name(op, shape, dtype), "selected": result.entry.kernel_name,
+                           "latencies_us": {k: round(v * 1e3, 2) for k, v in lat.items()}})
+        if not quiet:
+            print(f"[sweep] {op:17s} {str(shape):22s} {str(dtype)[6:]:9s} -> {result.entry.kernel_name:22s} "
+                  + " ".join(f"{k}={v * 1e3:.1f}us" for k, v in lat.items()), flush=True)
         del tensors
     out_dir.mkdir(parents=True, exist_ok=True)
     for op, report in reports.items():
@@ -131,7 +155,8 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
             report.attach_counters(counters)
         save_report(report, out_dir / f"selection_{op}.json")
     summary = {"cells": total, "hip_selected": wins, "hip_win_rate": round(wins / total, 4) if total else None,
-               "gpu": info.device_name}
+               "decode_cells": decode_total, "decode_hip_selected": decode_wins,
+               "not_hip": others, "gpu": info.device_name, "cache_key": info.cache_key}
     (out_dir / "selection_summary.json").write_text(json.dumps(summary, indent=2))
     return summary
 

@@ -35,9 +35,39 @@ def _timed(fn) -> tuple[Any, float]:
     return out, (time.perf_counter() - t0) * 1e3
 
 
+def graphed_step_breakdown(model, prompt: torch.Tensor, steps: int = 32) -> dict[str, Any]:
+    """Where a graph-replayed decode step's device time goes: ``steps`` replays
+    recorded with ``torch.profiler`` and folded by kernel name, with the share
+    of this library's kernels (``ako::``). Profiling adds a little time per
+    kernel, so the totals here run above the untraced step time."""
+    from ako_amd.benchmark.profiler import kernel_table, library_share, profile_cuda
+
+    runner = GraphedGreedy(model, prompt, steps + 1)
+    torch.cuda.synchronize()
+    with profile_cuda() as prof:
+        runner.run()
+        torch.cuda.synchronize()
+    rows = kernel_table(prof, device=True)
+    share = library_share(rows)
+    del runner
+    if not rows or share["total_us"] <= 0:
+        return {"steps": steps, "recorded": False}
+    return {
+        "steps": steps,
+        "recorded": True,
+        "device_us_per_step": round(share["total_us"] / steps, 1),
+        "library_us_per_step": round(share["library_us"] / steps, 1),
+        "library_share": round(share["share"], 4),
+        "library_launches_per_step": round(share["library_calls"] / steps, 2),
+        "library_kernels": share["library_kernels"],
+        "top": [{"name": r["name"][:80], "us_per_step": round(r["total_us"] / steps, 2),
+                 "calls_per_step": round(r["calls"] / steps, 2)} for r in rows[:8]],
+    }
+
+
 def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3,
                 device: str = "cuda", seed: int = 0, graphed: bool = True, prefill_warmup: int = 3,
-                prefill_repeats: int = 20) -> dict[str, Any]:
+                prefill_repeats: int = 20, breakdown: bool = False) -> dict[str, Any]:
     cfg = config5()
     cfg.max_seq_len = prompt_len + decode_steps
     model = build_lm(cfg, backend=backend, device=device, dtype=torch.float16, seed=seed)
@@ -76,6 +106,7 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
                 graphed_tokens, t_g = _timed(runner.run)
                 graphed_ms.append(t_g)
                 del runner
+        step_breakdown = graphed_step_breakdown(model, prompt) if (graphed and breakdown) else None
     prefill = sorted(prefill_ms)[len(prefill_ms) // 2]
     dec = sorted(decode_ms)[len(decode_ms) // 2]
     extra = {}
@@ -96,11 +127,13 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
         "decode_steps": decode_steps,
         "tokens": tokens[0].tolist(),
         **extra,
+        **({"graphed_step_breakdown": step_breakdown} if step_breakdown is not None else {}),
     }
 
 
 def compare(prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3) -> dict[str, Any]:
-    results = {b: run_config5(b, prompt_len=prompt_len, decode_steps=decode_steps, repeats=repeats)
+    results = {b: run_config5(b, prompt_len=prompt_len, decode_steps=decode_steps, repeats=repeats,
+                              breakdown=(b == "ako"))
                for b in ("torch", "ako")}
     ta, tt = results["ako"]["tokens"], results["torch"]["tokens"]
     first_diff = next((i for i, (a, b) in enumerate(zip(ta, tt)) if a != b), None)

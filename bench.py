@@ -4,28 +4,41 @@
 One *step* is one pass of the hot path over the BASELINE.json configs[1]
 prefill grid: plain RMSNorm and residual-add RMSNorm, fp16 and bf16, hidden
 4096 / 8192 / 16384, 16384 rows (12 kernel launches, 11.27 GB of algorithmic
-traffic). Inputs are resident in HBM before timing starts; consecutive
-launches touch different buffers (11 GB per step against a 256 MB Infinity
-Cache), so every launch reads cold data. ``value`` is algorithmic bytes per
-step x steps / elapsed device time, in GB/s.
+traffic). Inputs are resident in HBM before timing starts. Every launch of a
+step reads buffers of its own (the plain and the residual launch of a width
+do not share x), 11 GB per step against a 256 MB Infinity Cache, so every
+launch reads cold data. ``value`` is algorithmic bytes per step x steps /
+elapsed device time, in GB/s.
 
 Also reported on the same line:
-  roofline      the dominant kernel (largest share of the step) with its
-                per-launch duration from HIP events on the launch stream,
-                and a plain device copy of the same byte count timed the same
-                way (copy_same_bytes: the size's practical ceiling);
-  per_kernel    every launch of the step;
+  roofline      the dominant kernel (the slowest launch of the step) with its
+                per-launch duration from HIP events on the launch stream, and
+                a plain device copy of the same byte count timed the same way
+                (copy_same_bytes: the size's practical ceiling);
+  per_kernel    every launch of the step, each beside its copy ceiling;
   extras        the RoPE and SwiGLU cells, the
                 decode-size RMSNorm cells, the KV-cache RoPE and the
-                tensor-parallel RMSNorm halves;
+                tensor-parallel RMSNorm halves; streaming cells beside their
+                copy ceiling, decode cells as graph-replayed device time with
+                inputs hot (graph_us) and in no cache (graph_cold_us);
+  rope_prefill  RoPE at (4, 2048) as the fused q+k launch, the way the
+                decoder runs it;
+  selection     the reference's selection (gate + timing + cache record) run
+                here over the configs[1]-[3] grid, decode cells included: how
+                many cells the HIP candidate won;
   decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
                 128 greedy steps, eager PyTorch vs the dispatcher, each also
                 with decode steps replayed from a HIP graph;
-  cpu_baseline  the oracle (numpy port of the reference's unfused path, one
-                thread) on the same grid with a bounded row sample, and beside
-                it the restated PyTorch reference on host CPU tensors.
+  cpu_baseline  the reference's unfused PyTorch path (rmsnorm_ref /
+                rmsnorm_residual_ref, restated) on host CPU tensors with all
+                of torch's threads, on the same 12 cells with a bounded row
+                sample; the numpy oracle on one thread beside it.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+``dtype`` is the arithmetic type of the kernels (fp32); the stored tensors
+are fp16 and bf16 (``config.storage_dtypes``).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
+       [--no-selection] [--no-decoder] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -34,6 +47,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -42,6 +56,8 @@ sys.path.insert(0, str(ROOT))
 
 RMS_HIDDEN = (4096, 8192, 16384)
 RMS_ROWS = 16384
+#: Cells at least this large are streaming cells, reported beside a copy of the same bytes.
+STREAMING_BYTES = 16 * 2**20
 
 
 def parse_args() -> argparse.Namespace:
@@ -50,6 +66,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="skip the RoPE/SwiGLU/decode cells")
+    ap.add_argument("--no-selection", action="store_true", help="skip the selection over the grid")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decoder", action="store_true", help="skip the configs[4] decoder run")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -60,6 +77,280 @@ def parse_args() -> argparse.Namespace:
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class CopyCeilings:
+    """Copy-of-the-same-bytes figures by byte count, each measured once."""
+
+    def __init__(self, rf) -> None:
+        self.rf = rf
+        self.seen: dict[int, dict | None] = {}
+
+    def get(self, alg_bytes: int) -> dict | None:
+        if alg_bytes not in self.seen:
+            self.seen[alg_bytes] = self.rf.copy_same_bytes(alg_bytes)
+        return self.seen[alg_bytes]
+
+    def annotate(self, row: dict, gbps: float) -> None:
+        copy = self.get(row["alg_bytes"])
+        if copy is not None:
+            row["copy_pct_hbm_peak"] = round(100 * copy["frac"], 2)
+            row["kernel_over_copy"] = round(gbps / copy["gbps"], 4)
+
+
+def headline(args, torch, rf, dev, peak, rnd):
+    """The metric's workload: configs[1] prefill grid, 12 launches per step."""
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+
+    calls = []
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        for h in RMS_HIDDEN:
+            x_plain = rnd(RMS_ROWS, h, dtype=dtype)
+            x_res = rnd(RMS_ROWS, h, dtype=dtype)
+            r = rnd(RMS_ROWS, h, dtype=dtype)
+            w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
+            calls.append((f"rmsnorm_{tag}_{RMS_ROWS}x{h}", rf.alg_bytes_rmsnorm(RMS_ROWS, h, dtype),
+                          lambda x=x_plain, w=w: rmsnorm_hip(x, w, 1e-6)))
+            calls.append((f"rmsnorm_residual_{tag}_{RMS_ROWS}x{h}",
+                          rf.alg_bytes_rmsnorm_residual(RMS_ROWS, h, dtype),
+                          lambda x=x_res, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
+    bytes_per_step = sum(b for _, b, _ in calls)
+    log(f"workload: {len(calls)} launches/step, {bytes_per_step / 1e9:.3f} GB/step, "
+        f"warmup {args.warmup}, steps {args.steps}")
+    rf.warm(calls, args.warmup)
+    total_ms = rf.time_steps(calls, steps=args.steps)
+    # The dominant kernel's launch duration: the same K steps again, now with an
+    # event pair around every launch (kept out of the region above so that the
+    # step time holds nothing but the kernels and their launches).
+    per_launch = rf.time_each_launch(calls, steps=args.steps)
+    del calls
+    torch.cuda.empty_cache()
+    return bytes_per_step, total_ms, per_launch
+
+
+def extras_cells(torch, rf, dev, rnd):
+    """(name, alg_bytes, [thunks over input copies], decode) for every extra cell."""
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+    from ako_amd.ops.rmsnorm_tp import rmsnorm_shard_apply_hip, rmsnorm_shard_partial_hip
+    from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
+    from ako_amd.ops.rope_ref import build_rope_tables
+    from ako_amd.ops.swiglu_hip import swiglu_hip
+
+    cells = []
+
+    def add(name, nbytes, make, copies, decode):
+        cells.append((name, nbytes, [make(i) for i in range(copies)], decode))
+
+    decode_copies = 64  # independent inputs for the cold graph (one per call)
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        for b, s in ((4, 2048), (64, 1), (1, 1)):
+            cos, sin = build_rope_tables(s, 128, device=dev)
+            cos, sin = cos.to(dtype), sin.to(dtype)
+            decode = s == 1
+            n = decode_copies if decode else rf.copies_for_cold(rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype), dev)
+            qs = [rnd(b, s, 32, 128, dtype=dtype) for _ in range(n)]
+            ks = [rnd(b, s, 8, 128, dtype=dtype) for _ in range(n)]
+            add(f"rope_q_{tag}_{b}x{s}x32x128", rf.alg_bytes_rope(b, s, 32, 128, dtype, dtype),
+                lambda i, c=cos, sn=sin, qs=qs: (lambda q=qs[i]: rope_hip(q, c, sn, "neox")), n, decode)
+            add(f"rope_k_{tag}_{b}x{s}x8x128", rf.alg_bytes_rope(b, s, 8, 128, dtype, dtype),
+                lambda i, c=cos, sn=sin, ks=ks: (lambda k=ks[i]: rope_hip(k, c, sn, "neox")), n, decode)
+            add(f"rope_qk_{tag}_{b}x{s}", rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype),
+                lambda i, c=cos, sn=sin, qs=qs, ks=ks: (lambda q=qs[i], k=ks[i]: rope_qk_hip(q, k, c, sn, "neox")),
+                n, decode)
+    # configs[4] decode step, one layer: RoPE of q and k plus the KV-cache
+    # append, fused (one launch) and as the unfused sequence it replaces.
+    dtype = torch.float16
+    full_cos, full_sin = build_rope_tables(640, 128, device=dev)
+    qkv = [tuple(rnd(1, 1, 32, 128, dtype=dtype) for _ in range(3)) for _ in range(decode_copies)]
+    kc, vc = rnd(1, 32, 640, 128, dtype=dtype), rnd(1, 32, 640, 128, dtype=dtype)
+    pos = torch.full((1,), 511, dtype=torch.long, device=dev)
+    cache_bytes = rf.alg_bytes_rope_qk_cache(1, 1, 32, 32, 128, dtype, torch.float32)
+
+    def unfused(i):
+        q1, k1, v1 = qkv[i]
+
+        def step():
+            c, sn = full_cos.index_select(0, pos), full_sin.index_select(0, pos)
+            qo, ko = rope_qk_hip(q1, k1, c, sn, "neox")
+            kc.index_copy_(2, pos, ko.transpose(1, 2))
+            vc.index_copy_(2, pos, v1.transpose(1, 2))
+            return qo
+        return step
+
+    add("rope_qk_cache_fp16_1x1_q32_kv32_slot511of640", cache_bytes,
+        lambda i: (lambda t=qkv[i]: rope_qk_cache_hip(t[0], t[1], t[2], full_cos, full_sin, pos, kc, vc, "neox")),
+        decode_copies, True)
+    add("rope_qk_then_index_copy_fp16_1x1_q32_kv32", cache_bytes, unfused, decode_copies, True)
+    # One tensor-parallel rank's slice of the widest configs[1] row (TP=8:
+    # 2048 of 16384): residual + partial sum of squares, then the apply half.
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        rows_tp, shard = RMS_ROWS, 2048
+        nb_p = rf.alg_bytes_rmsnorm_shard_partial(rows_tp, shard, dtype, residual=True)
+        nb_a = rf.alg_bytes_rmsnorm_shard_apply(rows_tp, shard, dtype)
+        n = rf.copies_for_cold(nb_p, dev)
+        xs = [rnd(rows_tp, shard, dtype=dtype) for _ in range(n)]
+        rs = [rnd(rows_tp, shard, dtype=dtype) for _ in range(n)]
+        w_tp = rnd(shard, dtype=dtype, scale=0.1, shift=1.0)
+        tot = torch.full((rows_tp,), float(shard), device=dev)
+        add(f"rmsnorm_shard_partial_{tag}_{rows_tp}x{shard}_residual", nb_p,
+            lambda i, xs=xs, rs=rs: (lambda x=xs[i], r=rs[i]: rmsnorm_shard_partial_hip(x, r)), n, False)
+        add(f"rmsnorm_shard_apply_{tag}_{rows_tp}x{shard}", nb_a,
+            lambda i, xs=xs, w=w_tp, t=tot, shard=shard:
+                (lambda s_=xs[i]: rmsnorm_shard_apply_hip(s_, w, t, 8 * shard, 1e-6)), n, False)
+    for m in (16384, 4096, 256, 16, 1):
+        dtype = torch.bfloat16
+        nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)
+        decode = m <= 16
+        n = decode_copies if decode else rf.copies_for_cold(nbytes, dev)
+        gs = [rnd(m, 14336, dtype=dtype) for _ in range(n)]
+        us = [rnd(m, 14336, dtype=dtype) for _ in range(n)]
+        add(f"swiglu_bf16_{m}x14336", nbytes, lambda i, gs=gs, us=us: (lambda g=gs[i], u=us[i]: swiglu_hip(g, u)),
+            n, decode)
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        for rows in (1, 32):
+            for h in RMS_HIDDEN:
+                sets = [(rnd(rows, h, dtype=dtype), rnd(rows, h, dtype=dtype),
+                         rnd(h, dtype=dtype, scale=0.1, shift=1.0)) for _ in range(decode_copies)]
+                add(f"rmsnorm_{tag}_{rows}x{h}", rf.alg_bytes_rmsnorm(rows, h, dtype),
+                    lambda i, sets=sets: (lambda t=sets[i]: rmsnorm_hip(t[0], t[2], 1e-6)), decode_copies, True)
+                add(f"rmsnorm_residual_{tag}_{rows}x{h}", rf.alg_bytes_rmsnorm_residual(rows, h, dtype),
+                    lambda i, sets=sets: (lambda t=sets[i]: rmsnorm_residual_hip(t[0], t[1], t[2], 1e-6)),
+                    decode_copies, True)
+    return cells
+
+
+def time_extras(cells, torch, rf, peak, ceilings):
+    """Each cell: 60 back-to-back launches over its input copies between one
+    event pair (per-launch events would distort 5-30 us kernels); streaming
+    cells beside the copy of the same bytes; decode cells also as device time
+    per call from replayed HIP graphs, inputs hot (64 calls on one input) and
+    cold (64 calls on 64 inputs after an eviction pass)."""
+    extras = []
+    for _, _, fns, _ in cells:
+        for fn in fns[:2]:
+            fn()
+    torch.cuda.synchronize()
+    for name, nbytes, fns, decode in cells:
+        if decode:
+            ms = rf.time_back_to_back(fns[:1], launches=60)  # hot: one input, as before
+        else:
+            ms = rf.time_back_to_back(fns, launches=60)
+        stats = rf.LaunchStats(name, nbytes, [ms])
+        row = stats.to_dict(peak)
+        row.pop("launches")
+        row.pop("p50_us")
+        row["copies"] = 1 if decode else len(fns)
+        if nbytes >= STREAMING_BYTES:
+            ceilings.annotate(row, stats.gbps())
+        if decode:
+            # Median of five graph timings: one is under a millisecond of
+            # device time, and clock changes move single readings by up to 15%.
+            row["graph_us"] = round(sorted(rf.time_graph_replay(fns[0]) for _ in range(5))[2], 3)
+            row["graph_cold_us"] = round(rf.time_graph_cold(fns), 3)
+        extras.append(row)
+    return extras
+
+
+def rope_prefill_summary(extras, ceilings):
+    """RoPE at the prefill shape as the decoder runs it: q and k in one launch."""
+    by_name = {r["name"]: r for r in extras}
+    out = {}
+    for tag in ("fp16", "bf16"):
+        qk = by_name.get(f"rope_qk_{tag}_4x2048")
+        k = by_name.get(f"rope_k_{tag}_4x2048x8x128")
+        if qk is None:
+            continue
+        out[tag] = {"cell": qk["name"], "pct_hbm_peak": qk["pct_hbm_peak"],
+                    "copy_pct_hbm_peak": qk.get("copy_pct_hbm_peak"), "kernel_over_copy": qk.get("kernel_over_copy")}
+        if k is not None:
+            out[tag]["k_alone"] = {"pct_hbm_peak": k["pct_hbm_peak"], "copy_pct_hbm_peak": k.get("copy_pct_hbm_peak"),
+                                   "note": "34 MB launch: bounded by the copy ceiling of that size"}
+    return out
+
+
+def selection(torch):
+    """The reference's Algorithm 1 over the configs[1]-[3] grid on this GPU."""
+    from ako_amd.benchmark.sweep import run
+
+    with tempfile.TemporaryDirectory(prefix="ako-selection-") as tmp:
+        summary = run(Path(tmp), {"rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"},
+                      warmup=5, repeats=20, quiet=True)
+    summary["win_rate"] = summary.pop("hip_win_rate")
+    torch.cuda.empty_cache()
+    return summary
+
+
+def cpu_baseline(args, torch, rf, value):
+    """The reference's unfused PyTorch path on the host cores (the lead figure),
+    and the numpy oracle on one thread beside it, on a bounded row sample."""
+    import numpy as np
+
+    from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
+    from oracle import ops as oracle
+
+    def storage(t):
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).numpy().view(np.uint16)
+        return t.numpy()
+
+    def timed_passes(cells, seconds):
+        for _, fn in cells:
+            fn()
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for _, fn in cells:
+                fn()
+            passes += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= seconds and passes >= 3:
+                return passes, elapsed
+
+    torch_rows, port_rows = 512, 64
+    g = torch.Generator().manual_seed(0)
+    torch_cells, port_cells = [], []
+    for dtype in (torch.float16, torch.bfloat16):
+        name = "float16" if dtype == torch.float16 else "bfloat16"
+        for h in RMS_HIDDEN:
+            x = torch.randn(torch_rows, h, generator=g).to(dtype)
+            r = torch.randn(torch_rows, h, generator=g).to(dtype)
+            w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
+            torch_cells.append((rf.alg_bytes_rmsnorm(torch_rows, h, dtype), lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
+            torch_cells.append((rf.alg_bytes_rmsnorm_residual(torch_rows, h, dtype),
+                                lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
+            xn, rn, wn = storage(x[:port_rows]), storage(r[:port_rows]), storage(w)
+            port_cells.append((rf.alg_bytes_rmsnorm(port_rows, h, dtype),
+                               lambda xn=xn, wn=wn, name=name: oracle.rmsnorm(xn, wn, 1e-6, dtype=name)))
+            port_cells.append((rf.alg_bytes_rmsnorm_residual(port_rows, h, dtype),
+                               lambda xn=xn, rn=rn, wn=wn, name=name:
+                               oracle.rmsnorm_residual(xn, rn, wn, 1e-6, dtype=name)))
+    threads = torch.get_num_threads()
+    t_passes, t_elapsed = timed_passes(torch_cells, args.cpu_seconds)
+    torch_gbps = sum(b for b, _ in torch_cells) * t_passes / t_elapsed / 1e9
+    p_passes, p_elapsed = timed_passes(port_cells, args.cpu_seconds / 2)
+    port_gbps = sum(b for b, _ in port_cells) * p_passes / p_elapsed / 1e9
+    log(f"cpu baseline: PyTorch unfused reference {torch_gbps:.3f} GB/s on {threads} threads; "
+        f"numpy oracle {port_gbps:.3f} GB/s on 1 thread")
+    return {
+        "value": round(torch_gbps, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"the reference's unfused PyTorch path (rmsnorm_ref / rmsnorm_residual_ref, "
+                   f"ako/ops/rmsnorm_ref.py:8-50 restated) on host CPU tensors with torch's "
+                   f"{threads} threads, os.cpu_count()={os.cpu_count()}: the same 12 cells with "
+                   f"{torch_rows} rows instead of {RMS_ROWS}, {t_passes} passes in {t_elapsed:.1f} s"),
+        "gpu_speedup": round(value / torch_gbps, 1) if torch_gbps > 0 else None,
+        "oracle_numpy": {
+            "value": round(port_gbps, 3),
+            "cores": 1,
+            "sample": (f"oracle.ops.rmsnorm / rmsnorm_residual (numpy, one thread), same cells with "
+                       f"{port_rows} rows: {p_passes} passes in {p_elapsed:.1f} s"),
+        },
+    }
 
 
 def main() -> int:
@@ -78,10 +369,6 @@ def main() -> int:
         return 1
     from ako_amd import _native
     from ako_amd.benchmark import roofline as rf
-    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
-    from ako_amd.ops.rope_hip import rope_hip, rope_qk_cache_hip, rope_qk_hip
-    from ako_amd.ops.rope_ref import build_rope_tables
-    from ako_amd.ops.swiglu_hip import swiglu_hip
 
     _native.load()
     dev = torch.device("cuda", 0)
@@ -92,33 +379,17 @@ def main() -> int:
     def rnd(*shape, dtype, scale=1.0, shift=0.0):
         return (torch.randn(*shape, generator=gen, device=dev) * scale + shift).to(dtype)
 
-    # ---- the metric's workload: configs[1] prefill grid ------------------------
-    calls = []
-    for dtype in (torch.float16, torch.bfloat16):
-        tag = "fp16" if dtype == torch.float16 else "bf16"
-        for h in RMS_HIDDEN:
-            x = rnd(RMS_ROWS, h, dtype=dtype)
-            r = rnd(RMS_ROWS, h, dtype=dtype)
-            w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
-            calls.append((f"rmsnorm_{tag}_{RMS_ROWS}x{h}", rf.alg_bytes_rmsnorm(RMS_ROWS, h, dtype),
-                          lambda x=x, w=w: rmsnorm_hip(x, w, 1e-6)))
-            calls.append((f"rmsnorm_residual_{tag}_{RMS_ROWS}x{h}",
-                          rf.alg_bytes_rmsnorm_residual(RMS_ROWS, h, dtype),
-                          lambda x=x, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
-    bytes_per_step = sum(b for _, b, _ in calls)
-    log(f"workload: {len(calls)} launches/step, {bytes_per_step / 1e9:.3f} GB/step, "
-        f"warmup {args.warmup}, steps {args.steps}")
-    rf.warm(calls, args.warmup)
-    total_ms = rf.time_steps(calls, steps=args.steps)
+    bytes_per_step, total_ms, per_launch = headline(args, torch, rf, dev, peak, rnd)
     ms_per_step = total_ms / args.steps
     value = bytes_per_step * args.steps / (total_ms * 1e-3) / 1e9
     log(f"timed: {ms_per_step:.3f} ms/step, {value:.1f} GB/s ({100 * value / peak:.1f}% of {peak:.0f})")
-    # The dominant kernel's launch duration: the same K steps again, now with an
-    # event pair around every launch (kept out of the region above so that the
-    # step time holds nothing but the kernels and their launches).
-    per_launch = rf.time_each_launch(calls, steps=args.steps)
     dominant = max(per_launch, key=lambda s: s.mean_ms)
-    per_kernel = [s.to_dict(peak) for s in per_launch]
+    ceilings = CopyCeilings(rf)
+    per_kernel = []
+    for stats in per_launch:
+        row = stats.to_dict(peak)
+        ceilings.annotate(row, stats.gbps())
+        per_kernel.append(row)
 
     roofline = {
         "bound": "hbm",
@@ -143,7 +414,7 @@ def main() -> int:
         for row in per_kernel:
             if row["name"] in measured:
                 row["traffic_bytes"] = measured[row["name"]]
-    copy = rf.copy_same_bytes(dominant.alg_bytes)
+    copy = ceilings.get(dominant.alg_bytes)
     if copy is not None:
         roofline["copy_same_bytes"] = {
             "gbps": copy["gbps"],
@@ -155,116 +426,29 @@ def main() -> int:
         }
         log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
             f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")
-    del calls
-    torch.cuda.empty_cache()
 
-    # ---- other configs' cells (reported, not the metric) ----------------------
-    extras = []
-    launch_floor = None
+    extras, launch_floor, rope_prefill = [], None, None
     if not args.no_extras:
-        cells = []
-        for dtype in (torch.float16, torch.bfloat16):
-            tag = "fp16" if dtype == torch.float16 else "bf16"
-            for b, s in ((4, 2048), (64, 1), (1, 1)):
-                cos, sin = build_rope_tables(s, 128, device=dev)
-                cos, sin = cos.to(dtype), sin.to(dtype)
-                copies = rf.copies_for_cold(rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype), dev) if s > 1 else 1
-                qs = [rnd(b, s, 32, 128, dtype=dtype) for _ in range(copies)]
-                ks = [rnd(b, s, 8, 128, dtype=dtype) for _ in range(copies)]
-                for i in range(copies):
-                    cells.append((f"rope_q_{tag}_{b}x{s}x32x128", rf.alg_bytes_rope(b, s, 32, 128, dtype, dtype),
-                                  lambda q=qs[i], c=cos, sn=sin: rope_hip(q, c, sn, "neox")))
-                    cells.append((f"rope_k_{tag}_{b}x{s}x8x128", rf.alg_bytes_rope(b, s, 8, 128, dtype, dtype),
-                                  lambda k=ks[i], c=cos, sn=sin: rope_hip(k, c, sn, "neox")))
-                    cells.append((f"rope_qk_{tag}_{b}x{s}", rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype),
-                                  lambda q=qs[i], k=ks[i], c=cos, sn=sin: rope_qk_hip(q, k, c, sn, "neox")))
-        # configs[4] decode step, one layer: RoPE of q and k plus the KV-cache
-        # append, fused (one launch) and as the unfused sequence it replaces.
-        dtype = torch.float16
-        full_cos, full_sin = build_rope_tables(640, 128, device=dev)
-        q1, k1, v1 = rnd(1, 1, 32, 128, dtype=dtype), rnd(1, 1, 32, 128, dtype=dtype), rnd(1, 1, 32, 128, dtype=dtype)
-        kc, vc = rnd(1, 32, 640, 128, dtype=dtype), rnd(1, 32, 640, 128, dtype=dtype)
-        pos = torch.full((1,), 511, dtype=torch.long, device=dev)
-        cache_bytes = rf.alg_bytes_rope_qk_cache(1, 1, 32, 32, 128, dtype, torch.float32)
-
-        def unfused_cache_step():
-            c, sn = full_cos.index_select(0, pos), full_sin.index_select(0, pos)
-            qo, ko = rope_qk_hip(q1, k1, c, sn, "neox")
-            kc.index_copy_(2, pos, ko.transpose(1, 2))
-            vc.index_copy_(2, pos, v1.transpose(1, 2))
-            return qo
-
-        cells.append(("rope_qk_cache_fp16_1x1_q32_kv32_slot511of640", cache_bytes,
-                      lambda: rope_qk_cache_hip(q1, k1, v1, full_cos, full_sin, pos, kc, vc, "neox")))
-        cells.append(("rope_qk_then_index_copy_fp16_1x1_q32_kv32", cache_bytes, unfused_cache_step))
-        # One tensor-parallel rank's slice of the widest configs[1] row (TP=8:
-        # 2048 of 16384): residual + partial sum of squares, then the apply half.
-        from ako_amd.ops.rmsnorm_tp import rmsnorm_shard_apply_hip, rmsnorm_shard_partial_hip
-
-        for dtype in (torch.float16, torch.bfloat16):
-            tag = "fp16" if dtype == torch.float16 else "bf16"
-            rows_tp, shard = RMS_ROWS, 2048
-            nb_p = rf.alg_bytes_rmsnorm_shard_partial(rows_tp, shard, dtype, residual=True)
-            nb_a = rf.alg_bytes_rmsnorm_shard_apply(rows_tp, shard, dtype)
-            copies = rf.copies_for_cold(nb_p, dev)
-            xs_tp = [rnd(rows_tp, shard, dtype=dtype) for _ in range(copies)]
-            rs_tp = [rnd(rows_tp, shard, dtype=dtype) for _ in range(copies)]
-            w_tp = rnd(shard, dtype=dtype, scale=0.1, shift=1.0)
-            tot = torch.full((rows_tp,), float(shard), device=dev)
-            for i in range(copies):
-                cells.append((f"rmsnorm_shard_partial_{tag}_{rows_tp}x{shard}_residual", nb_p,
-                              lambda x=xs_tp[i], r=rs_tp[i]: rmsnorm_shard_partial_hip(x, r)))
-                cells.append((f"rmsnorm_shard_apply_{tag}_{rows_tp}x{shard}", nb_a,
-                              lambda s_=xs_tp[i], w_=w_tp, t_=tot: rmsnorm_shard_apply_hip(s_, w_, t_, 8 * shard, 1e-6)))
-        for m in (16384, 4096, 256, 16, 1):
-            dtype = torch.bfloat16
-            nbytes = rf.alg_bytes_swiglu(m, 14336, dtype)
-            copies = rf.copies_for_cold(nbytes, dev) if m >= 256 else 1
-            gs = [rnd(m, 14336, dtype=dtype) for _ in range(copies)]
-            us = [rnd(m, 14336, dtype=dtype) for _ in range(copies)]
-            for i in range(copies):
-                cells.append((f"swiglu_bf16_{m}x14336", nbytes, lambda g=gs[i], u=us[i]: swiglu_hip(g, u)))
-        for dtype in (torch.float16, torch.bfloat16):
-            tag = "fp16" if dtype == torch.float16 else "bf16"
-            for rows in (1, 32):
-                for h in RMS_HIDDEN:
-                    x, r = rnd(rows, h, dtype=dtype), rnd(rows, h, dtype=dtype)
-                    w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
-                    cells.append((f"rmsnorm_{tag}_{rows}x{h}", rf.alg_bytes_rmsnorm(rows, h, dtype),
-                                  lambda x=x, w=w: rmsnorm_hip(x, w, 1e-6)))
-                    cells.append((f"rmsnorm_residual_{tag}_{rows}x{h}",
-                                  rf.alg_bytes_rmsnorm_residual(rows, h, dtype),
-                                  lambda x=x, r=r, w=w: rmsnorm_residual_hip(x, r, w, 1e-6)))
-        rf.warm(cells, 2)
-        # Each cell: 60 back-to-back launches over its input copies between one
-        # event pair (per-launch events would distort 5-30 us kernels), and for
-        # decode-size cells the device time per call from a replayed HIP graph
-        # of 64 launches (no host overhead), the median of five such timings.
-        groups: dict[str, list] = {}
-        for name, nbytes, fn in cells:
-            groups.setdefault(name, [nbytes, []])[1].append(fn)
-        for name, (nbytes, fns) in groups.items():
-            ms = rf.time_back_to_back(fns, launches=60)
-            stats = rf.LaunchStats(name, nbytes, [ms])
-            row = stats.to_dict(peak)
-            row.pop("launches")
-            row.pop("p50_us")
-            row["copies"] = len(fns)
-            if nbytes < 64 * 2**20:
-                # Median of five graph timings: one is under a millisecond of
-                # device time, and clock changes move single readings by up to 15%.
-                row["graph_us"] = round(sorted(rf.time_graph_replay(fns[0]) for _ in range(5))[2], 3)
-            extras.append(row)
-        # The floor those graph_us figures sit on: a graph-replayed launch of a
+        cells = extras_cells(torch, rf, dev, rnd)
+        extras = time_extras(cells, torch, rf, peak, ceilings)
+        del cells
+        torch.cuda.empty_cache()
+        rope_prefill = rope_prefill_summary(extras, ceilings)
+        # The floor the graph_us figures sit on: a graph-replayed launch of a
         # kernel that does nothing measurable (torch's add_ on one element).
         tiny = torch.zeros(1, device=dev)
         launch_floor = {"graph_us": round(sorted(rf.time_graph_replay(lambda: tiny.add_(1.0)) for _ in range(5))[2], 3),
                         "kernel": "torch add_ on one element, 64 launches per graph, replayed"}
         log(f"extras: {len(extras)} cells timed; graph launch floor {launch_floor['graph_us']} us")
-        del cells
-        torch.cuda.empty_cache()
 
-    # ---- the 4-layer decoder, prefill 512 + 128 greedy steps -------
+    picked = None
+    if not args.no_selection:
+        t0 = time.perf_counter()
+        picked = selection(torch)
+        log(f"selection: HIP chosen in {picked['hip_selected']} of {picked['cells']} cells "
+            f"({picked['decode_hip_selected']} of {picked['decode_cells']} decode cells) "
+            f"in {time.perf_counter() - t0:.0f} s")
+
     decoder = None
     if not args.no_decoder:
         from ako_amd.models.bench_decoder import compare
@@ -275,75 +459,7 @@ def main() -> int:
             f"(graphed {decoder['ako'].get('graphed_decode_ms_per_step')} ms)")
         torch.cuda.empty_cache()
 
-    # ---- CPU baseline: the oracle (a CPU port of the reference's algorithm) ------
-    # The oracle (numpy, single-threaded) is the primary figure, as a "port" of
-    # the reference's unfused path; the restated PyTorch reference on host
-    # tensors (multi-threaded) is reported beside it. Both run the 12 cells of
-    # the step on a bounded row sample, timed by wall clock for ~cpu-seconds.
-    cpu = None
-    if not args.no_cpu:
-        import numpy as np
-
-        from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
-        from oracle import ops as oracle
-
-        def storage(t: "torch.Tensor") -> "np.ndarray":
-            if t.dtype == torch.bfloat16:
-                return t.view(torch.int16).numpy().view(np.uint16)
-            return t.numpy()
-
-        def timed_passes(cells: list, seconds: float) -> tuple[int, float]:
-            for _, fn in cells:
-                fn()
-            passes, t0 = 0, time.perf_counter()
-            while True:
-                for _, fn in cells:
-                    fn()
-                passes += 1
-                elapsed = time.perf_counter() - t0
-                if elapsed >= seconds and passes >= 3:
-                    return passes, elapsed
-
-        sample_rows = 64
-        g = torch.Generator().manual_seed(0)
-        port_cells, torch_cells = [], []
-        for dtype in (torch.float16, torch.bfloat16):
-            name = "float16" if dtype == torch.float16 else "bfloat16"
-            for h in RMS_HIDDEN:
-                x = torch.randn(sample_rows, h, generator=g).to(dtype)
-                r = torch.randn(sample_rows, h, generator=g).to(dtype)
-                w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
-                xn, rn, wn = storage(x), storage(r), storage(w)
-                b_plain = rf.alg_bytes_rmsnorm(sample_rows, h, dtype)
-                b_res = rf.alg_bytes_rmsnorm_residual(sample_rows, h, dtype)
-                port_cells.append((b_plain, lambda xn=xn, wn=wn, name=name: oracle.rmsnorm(xn, wn, 1e-6, dtype=name)))
-                port_cells.append((b_res, lambda xn=xn, rn=rn, wn=wn, name=name:
-                                   oracle.rmsnorm_residual(xn, rn, wn, 1e-6, dtype=name)))
-                torch_cells.append((b_plain, lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
-                torch_cells.append((b_res, lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
-        passes, elapsed = timed_passes(port_cells, args.cpu_seconds)
-        port_gbps = sum(b for b, _ in port_cells) * passes / elapsed / 1e9
-        t_passes, t_elapsed = timed_passes(torch_cells, args.cpu_seconds / 2)
-        torch_gbps = sum(b for b, _ in torch_cells) * t_passes / t_elapsed / 1e9
-        cpu = {
-            "value": round(port_gbps, 3),
-            "unit": "GB/s",
-            "cores": 1,
-            "kind": "port",
-            "sample": (f"oracle.ops.rmsnorm / rmsnorm_residual (numpy restatement of the reference's "
-                       f"unfused path, one thread) on the same 12 cells with {sample_rows} rows instead "
-                       f"of {RMS_ROWS}: {passes} passes in {elapsed:.1f} s"),
-            "gpu_speedup": round(value / port_gbps, 1) if port_gbps > 0 else None,
-            "torch_cpu": {
-                "value": round(torch_gbps, 3),
-                "cores": torch.get_num_threads(),
-                "sample": (f"ako_amd.ops.rmsnorm_ref / rmsnorm_residual_ref (the reference's PyTorch "
-                           f"path) on host tensors, same cells: {t_passes} passes in {t_elapsed:.1f} s; "
-                           f"os.cpu_count()={os.cpu_count()}"),
-            },
-        }
-        log(f"cpu baseline: oracle {port_gbps:.3f} GB/s on 1 thread, torch CPU {torch_gbps:.3f} GB/s "
-            f"on {torch.get_num_threads()} threads")
+    cpu = None if args.no_cpu else cpu_baseline(args, torch, rf, value)
 
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op/shape; 4-layer decoder prefill+decode ms",
@@ -370,7 +486,9 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "selection": picked,
         "decoder": decoder,
+        "rope_prefill": rope_prefill,
         "per_kernel": per_kernel,
         "extras": extras,
         "launch_floor": launch_floor,

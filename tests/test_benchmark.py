@@ -14,16 +14,20 @@ import torch
 from ako_amd.benchmark import roofline as rf
 from ako_amd.benchmark.bench_op import (
     MAX_INNER_ITERS,
+    MAX_RING_COPIES,
     UNSTABLE_CV,
     BenchResult,
+    InputRing,
     bench_op,
     bootstrap_ci,
     bootstrap_ratio_ci,
     compare_paired,
     parse_dtypes,
+    percentile,
+    ring_state,
 )
 from ako_amd.benchmark.env import host_cpu, sample_env
-from ako_amd.benchmark.graph import try_capture
+from ako_amd.benchmark.graph import capture_calls
 from ako_amd.benchmark.report import BenchmarkReport
 from ako_amd.dispatcher.hardware import get_device_info
 from ako_amd.ops.rmsnorm_ref import rmsnorm_ref
@@ -156,10 +160,52 @@ def test_bench_line_regression_diff(tmp_path) -> None:
 
 
 def test_graph_capture_is_a_noop_on_cpu() -> None:
-    cap = try_capture(lambda t: t @ t, (torch.randn(8, 8),))
-    assert (cap.captured, cap.replay, cap.reason) == (False, None, "not_cuda")
+    cap = capture_calls(lambda t: t @ t, [(torch.randn(8, 8),)])
+    assert cap.graph is None and cap.calls == 0 and "not on a GPU" in cap.reason
+    with pytest.raises(RuntimeError, match="nothing was captured"):
+        cap.replay()
+    assert capture_calls(lambda t: t, []).reason == "no calls to capture"
     r = bench_op(lambda t: t @ t, (torch.randn(16, 16),), warmup=1, repeats=2, graph=True)
     assert r.graph_captured == 0
+
+
+def test_input_ring_rotates_copies_of_contiguous_tensors() -> None:
+    x, w = torch.randn(3, 5), torch.randn(5)
+    strided = torch.randn(4, 10)[:, ::2]
+    ring = InputRing((x, w, strided, 7), 4)
+    assert len(ring) == 4 and ring.shared == 1
+    seen = [ring.next() for _ in range(5)]
+    assert seen[0][0] is x and seen[4][0] is x  # entry 0 is the caller's, then it wraps
+    for entry in seen[1:4]:
+        assert torch.equal(entry[0], x) and entry[0].data_ptr() != x.data_ptr()
+        assert torch.equal(entry[1], w) and entry[1].data_ptr() != w.data_ptr()
+        assert entry[2] is strided and entry[3] == 7  # strided and non-tensors are shared
+    assert len({e[0].data_ptr() for e in seen[:4]}) == 4
+    assert InputRing((x,), 1).entries == [(x,)]
+
+
+def test_ring_state_and_percentile() -> None:
+    l2, mall = 32 << 20, 256 << 20
+    assert ring_state(2 * (l2 + mall), l2, mall) == "cold"
+    assert ring_state(2 * l2, l2, mall) == "l2-cold"
+    assert ring_state(l2, l2, mall) == "warm"
+    assert MAX_RING_COPIES >= 256
+    assert percentile([], 0.5) == 0.0
+    assert percentile([3.0, 1.0, 2.0], 0.5) == 2.0
+    assert percentile([1.0, 2.0, 3.0, 4.0], 0.5) == 2.0  # nearest rank: lower median
+    assert percentile([1.0, 2.0, 3.0, 4.0], 0.95) == 4.0 and percentile([5.0], 0.0) == 5.0
+
+
+def test_compare_paired_sees_a_real_difference() -> None:
+    x, w = torch.randn(64, 4096), torch.ones(4096)
+
+    def slow(a, b):
+        for _ in range(4):
+            rmsnorm_ref(a, b)
+
+    out = compare_paired(slow, rmsnorm_ref, (x, w), pairs=5, warmup=1, repeats=4)
+    assert out["speedup_median"] > 2.0 and out["significant"]
+    assert out["speedup_ci95"][0] <= out["speedup_median"] <= out["speedup_ci95"][1]
 
 
 def test_roofline_bytes_and_peaks() -> None:

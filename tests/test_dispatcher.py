@@ -255,7 +255,7 @@ def test_driver_label_prefers_the_module_version() -> None:
 def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
     """The reset/clear helpers the reference exposes for tests, and
     ``load_baseline`` for its regression diffs, behave as their names say."""
-    from ako_amd.benchmark.profiler import profile_cuda
+    from ako_amd.benchmark.profiler import kernel_table, profile_cuda
     from ako_amd.dispatcher import hardware
     from ako_amd.ops import _registry, rmsnorm_torch
     from ako_amd.validation.regression import load_baseline
@@ -284,3 +284,19 @@ def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
     with profile_cuda() as prof:
         torch.ones(4).sum()
     assert any("sum" in e.name for e in prof.events())
+    rows = kernel_table(prof)  # host op time on a CPU-only run
+    assert rows and any("sum" in r["name"] for r in rows)
+    assert abs(sum(r["share"] for r in rows) - 1.0) < 1e-9
+
+
+def test_library_share_counts_ako_kernels() -> None:
+    from ako_amd.benchmark.profiler import library_share, table_markdown
+
+    rows = [{"name": "void ako::rmsnorm_reg<_Float16, 4, 2>(ako::RmsDev)", "calls": 9, "total_us": 30.0, "share": 0.3},
+            {"name": "Cijk_Alik_Bljk_HHS_BH", "calls": 29, "total_us": 60.0, "share": 0.6},
+            {"name": "_ZN3ako11swiglu_flatIDF16_Li1ELi256EEEvPKT_S3_PS1_lll", "calls": 4, "total_us": 10.0,
+             "share": 0.1}]
+    share = library_share(rows)
+    assert share["share"] == 0.4 and share["library_calls"] == 13 and len(share["library_kernels"]) == 2
+    md = table_markdown(rows, per=1)
+    assert md.count("\n") == 4 and "30.0" in md
