@@ -148,6 +148,11 @@ int ako_set_tuning(int op, int key, int value) {
       }
       if (key == 6) { ako::g_rms_tuning.xcd_chunk = value; return AKO_OK; }
       if (key == 7) { ako::g_rms_tuning.max_blocks = value; return AKO_OK; }
+      if (key == 8) {
+        if (value > 2) return fail(AKO_ERR_INVALID_ARGUMENT, "early weights must be 0, 1 or 2");
+        ako::g_rms_tuning.early_weights = value;
+        return AKO_OK;
+      }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

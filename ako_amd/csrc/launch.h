@@ -22,6 +22,7 @@ struct RmsTuning {
   int row_order = 0;        // key 5: 1 = rows in block order, 2 = XCD-blocked order
   int xcd_chunk = 0;        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
   int max_blocks = 0;       // key 7: cap on workgroups per launch (0 = 2^31 work-items)
+  int early_weights = 0;    // key 8: 1 = weights after the row's loads return, 2 = with them (0 = by launch size)
 };
 struct RopeTuning {
   int tokens_per_block = 0;  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)

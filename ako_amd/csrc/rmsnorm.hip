@@ -72,7 +72,7 @@ __device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, unsigned
   return full * 8 * chunk + x * rest + (i - full * chunk);
 }
 
-template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS>
+template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS, bool EW>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     T* __restrict__ y, T* __restrict__ rout, int64_t row0, int64_t rows, int hidden, int64_t sx,
@@ -87,7 +87,12 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   static_assert(VPT % G == 0, "VPT must be a multiple of the group size");
   // With few packets per lane the first weight group is fetched before the
   // reduction; with many, registers are kept for x and weights come per group.
-  constexpr bool kPrefetchW = AKO_RMS_PREFETCH_W != 0 && VPT <= 4;
+  // EW (early weights, decode-sized launches) issues the first weight group in
+  // the same batch as the row's own loads: a launch of a few rows is one
+  // dependent chain, and a norm weight that the rest of a model step has
+  // evicted then costs one HBM round trip instead of a second one after x.
+  static_assert(!EW || VPT <= 4, "early weights need the first group's weights in registers");
+  constexpr bool kPrefetchW = (AKO_RMS_PREFETCH_W != 0 || EW) && VPT <= 4;
   using P = Pack<T, E>;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -104,6 +109,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   T* yr = y + row * sy;
 
   P v[VPT];
+  WeightPacket<W, E> wv[G];
   float ss = 0.f;
 #pragma unroll
   for (int g0 = 0; g0 < VPT; g0 += G) {
@@ -114,6 +120,15 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
       if (active && vi < nvec) {
         v[g0 + k] = load_pack<T, E, NTL>(xr + vi * E);
         if constexpr (RES) rv[k] = load_pack<T, E, NTL>(res + row * sr + vi * E);
+      }
+    }
+    if constexpr (EW) {
+      if (g0 == 0) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+          const int vi = t + k * TPR;
+          if (active && vi < nvec) wv[k].load(w + vi * E);
+        }
       }
     }
 #pragma unroll
@@ -146,8 +161,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
 
   // The weight row is L2-resident (every row reads it); fetch the first group
   // before the reduction so its latency hides behind the cross-lane sums.
-  WeightPacket<W, E> wv[G];
-  if constexpr (kPrefetchW) {
+  if constexpr (kPrefetchW && !EW) {
 #pragma unroll
     for (int k = 0; k < G; ++k) {
       const int vi = t + k * TPR;
@@ -436,8 +450,8 @@ int64_t max_blocks_per_launch(int threads_per_block) {
   return forced > 0 ? std::min(cap, forced) : cap;
 }
 
-template <typename T, typename W, int WPR, int VPT, bool RES>
-hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
+template <typename T, typename W, int WPR, int VPT, bool RES, bool EW>
+hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
   const dim3 block(kWave * WPR * RPB);
   const int64_t total_blocks = ceil_div(a.rows, RPB);
@@ -462,7 +476,7 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
     if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
     if (g_rms_tuning.row_order == 2)
       xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
-    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0>), grid,
+    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0, EW>), grid,
                        block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                        static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                        b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
@@ -471,6 +485,30 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
     if (err != hipSuccess) return err;
   }
   return hipSuccess;
+}
+
+// Early weight loads (EW) for launches of at most kFewRows rows of at most
+// 8 KiB, whose time is one row's dependent chain. Graph-replayed on MI355X
+// with inputs evicted from every cache (64 calls on separate inputs after an
+// eviction pass), rows of 4096 half elements: residual 2.89 -> 2.64 us (1 row)
+// and 3.09 -> 2.94 us (32 rows), plain 2.50 -> 2.43 us; with hot inputs the
+// plain row gains 4% and the residual row loses 4%. Rows of 8192 and 16384
+// elements are 2-13% slower with early weights, hot and cold (more requests
+// per lane ahead of the reduction), so they keep the late loads, as do
+// launches of many rows, whose weight row is L2-resident after the first rows.
+// Only the one- and two-packet shapes (what decode rows use) have the variant.
+constexpr int64_t kEarlyWeightRowBytes = 8 * 1024;
+
+template <typename T, typename W, int WPR, int VPT, bool RES>
+hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
+  if constexpr (VPT <= 2) {
+    const int forced = g_rms_tuning.early_weights;
+    const bool ew = forced == 2 ||
+                    (forced == 0 && a.rows <= kFewRows &&
+                     a.hidden * static_cast<int64_t>(sizeof(T)) <= kEarlyWeightRowBytes);
+    if (ew) return run_reg_launch<T, W, WPR, VPT, RES, true>(a, stream);
+  }
+  return run_reg_launch<T, W, WPR, VPT, RES, false>(a, stream);
 }
 
 template <typename T, typename W, bool RES>

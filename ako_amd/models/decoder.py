@@ -171,10 +171,19 @@ class StaticKVCache:
     def length(self) -> int:
         return self.host_len
 
+    def set_length(self, length: int) -> None:
+        """Host-side: the first ``length`` slots are filled (after a prefill).
+        Sets ``pos`` and the mask: 0 for filled slots, -inf beyond."""
+        self.host_len = length
+        self.pos.fill_(length)
+        self.mask.fill_(float("-inf"))
+        self.mask[..., :length] = 0.0
+
     def begin_step(self) -> None:
-        """Refresh the attention mask from ``pos`` (device-side, capturable)."""
-        filled = self.slots <= self.pos
-        self.mask.copy_(torch.where(filled, 0.0, float("-inf")).to(self.mask.dtype).view(1, 1, 1, -1))
+        """Open slot ``pos`` in the attention mask for the token being decoded:
+        one device-side write per step (capturable). Slots below ``pos`` were
+        opened by earlier steps or by ``set_length``."""
+        self.mask.index_fill_(-1, self.pos, 0.0)
 
     def end_step(self, tokens: int) -> None:
         self.pos.add_(tokens)
@@ -409,8 +418,7 @@ class DecoderStack(nn.Module):
             if static_step:
                 kv_cache.end_step(1)
             else:
-                kv_cache.host_len += x.shape[1]
-                kv_cache.pos.fill_(kv_cache.host_len)
+                kv_cache.set_length(kv_cache.host_len + x.shape[1])
         return x
 
     def new_static_cache(self, max_len: int, *, batch: int = 1) -> StaticKVCache:
@@ -484,7 +492,10 @@ class GraphedGreedy:
         self.ids = model.logits_last(prompt, self.cache).argmax(-1, keepdim=True)
         self.history = torch.zeros(steps, dtype=torch.long, device=prompt.device)
         self.history[:1] = self.ids.view(1)
-        self.base = torch.full((1,), self.prompt_len - 1, dtype=torch.long, device=prompt.device)
+        # After a step, pos has advanced past the token just produced, whose
+        # index in history is pos - prompt_len.
+        self.base = torch.full((1,), self.prompt_len, dtype=torch.long, device=prompt.device)
+        self.slot = torch.zeros(1, dtype=torch.long, device=prompt.device)
 
         first = self.ids.clone()
         side = torch.cuda.Stream()
@@ -500,10 +511,10 @@ class GraphedGreedy:
             self._step()
 
     def _step(self) -> None:
-        nxt = self.model.logits_last(self.ids, self.cache).argmax(-1, keepdim=True)
-        self.ids.copy_(nxt)
-        # pos has advanced past the token just produced: its index is pos - prompt_len.
-        self.history.index_copy_(0, self.cache.pos - self.base - 1, nxt.view(1))
+        logits = self.model.logits_last(self.ids, self.cache)
+        torch.argmax(logits, -1, keepdim=True, out=self.ids)
+        torch.sub(self.cache.pos, self.base, out=self.slot)
+        self.history.index_copy_(0, self.slot, self.ids.view(1))
 
     @torch.no_grad()
     def run(self) -> torch.Tensor:

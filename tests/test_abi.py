@@ -188,7 +188,8 @@ def test_tuning_keys(lib) -> None:
     assert lib.ako_set_tuning(0, 1, -1) == INVALID
     assert lib.ako_set_tuning(0, 5, 3) == INVALID
     assert lib.ako_set_tuning(2, 2, 256) == INVALID  # SwiGLU has one key: packets per lane
-    for op, key in ((0, 1), (0, 2), (0, 3), (0, 4), (0, 5), (0, 6), (0, 7), (1, 1), (1, 2), (2, 1)):
+    assert lib.ako_set_tuning(0, 8, 3) == INVALID  # early weights: 0, 1 or 2
+    for op, key in ((0, 1), (0, 2), (0, 3), (0, 4), (0, 5), (0, 6), (0, 7), (0, 8), (1, 1), (1, 2), (2, 1)):
         assert lib.ako_set_tuning(op, key, 0) == OK
 
 

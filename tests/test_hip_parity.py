@@ -154,21 +154,28 @@ def test_rmsnorm_every_register_shape() -> None:
     w = grandn((4096,), torch.bfloat16, 11, scale=0.1, shift=1.0)
     expected = oracle.rmsnorm(to_np(x), to_np(w), dtype="bfloat16")
     ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype="bfloat16")
+    w32 = w.float()
+    expected32 = oracle.rmsnorm(to_np(x), to_np(w32), dtype="bfloat16", w_dtype="float32")
     shapes = [(1, 8), (2, 4), (2, 8), (4, 2), (4, 4), (4, 8), (8, 1), (8, 2), (8, 4), (8, 8), (16, 1), (16, 2), (16, 4), (16, 8)]
     try:
         for wpr, vpt in shapes:
             _native.set_tuning(0, 1, wpr)
             _native.set_tuning(0, 2, vpt)
-            assert_oracle(expected, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
-            y, s = rmsnorm_residual_hip(x, r, w)
-            np.testing.assert_array_equal(to_np(s), es)
-            assert_oracle(ey, to_np(y), torch.bfloat16)
-        _native.set_tuning(0, 1, 0)
-        _native.set_tuning(0, 2, 0)
+            # One- and two-packet shapes also come with early weight loads
+            # (key 8: 1 = late, 2 = early); the others ignore the key.
+            for early in ((1, 2) if vpt <= 2 else (0,)):
+                _native.set_tuning(0, 8, early)
+                assert_oracle(expected, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
+                assert_oracle(expected32, to_np(rmsnorm_hip(x, w32)), torch.bfloat16)
+                y, s = rmsnorm_residual_hip(x, r, w)
+                np.testing.assert_array_equal(to_np(s), es)
+                assert_oracle(ey, to_np(y), torch.bfloat16)
+        for key in (1, 2, 8):
+            _native.set_tuning(0, key, 0)
         _native.set_tuning(0, 3, 1)  # force the two-pass kernel
         assert_oracle(expected, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
     finally:
-        for key in (1, 2, 3):
+        for key in (1, 2, 3, 8):
             _native.set_tuning(0, key, 0)
 
 
