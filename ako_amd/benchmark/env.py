@@ -1,4 +1,4 @@
-"""GPU state next to a measurement: clock, temperature, power.
+"""GPU state next to a measurement: clock, temperature, power, idleness.
 
 The reference samples these through ``nvidia-smi`` (``ako/benchmark/env.py:80-119``).
 On ROCm the amdgpu driver exposes them in sysfs, which needs no subprocess:
@@ -6,6 +6,12 @@ On ROCm the amdgpu driver exposes them in sysfs, which needs no subprocess:
 hwmon ``temp*_input`` (millidegrees) / ``power1_average`` or ``power1_input``
 (microwatts). Every field is ``None`` when the file is missing, because a
 measurement without an environment sample is still a measurement.
+
+``preflight`` is the reference's busy-GPU check (``env.py:95-119``): other
+processes computing on the card, or a card already busy, make every latency
+measured after it meaningless. On ROCm the compute processes are the entries
+of the KFD's ``/sys/class/kfd/kfd/proc`` (one directory per process with a GPU
+context) and the load is the card's ``gpu_busy_percent``.
 """
 
 from __future__ import annotations
@@ -18,9 +24,10 @@ from typing import Any
 _DRM = Path("/sys/class/drm")
 
 
-def _gpu_device_dirs() -> list[Path]:
-    cards = sorted(p for p in _DRM.glob("card[0-9]*") if re.fullmatch(r"card\d+", p.name))
-    return [c / "device" for c in cards if (c / "device" / "pp_dpm_sclk").exists()]
+def _gpu_device_dirs(drm: Path = _DRM, marker: str = "pp_dpm_sclk") -> list[Path]:
+    """``cardN/device`` directories of the amdgpu cards that expose ``marker``."""
+    cards = sorted(p for p in drm.glob("card[0-9]*") if re.fullmatch(r"card\d+", p.name))
+    return [c / "device" for c in cards if (c / "device" / marker).exists()]
 
 
 def _read(path: Path) -> str | None:
@@ -78,3 +85,53 @@ def host_cpu() -> dict[str, Any]:
         pass
     affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
     return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity}
+
+
+_KFD_PROCS = Path("/sys/class/kfd/kfd/proc")
+#: Utilisation at or above which the card is taken to be busy (the reference's 3%).
+BUSY_PERCENT = 3.0
+
+
+def _busy_percent(dev: Path) -> float | None:
+    raw = _read(dev / "gpu_busy_percent")
+    try:
+        return float(raw) if raw is not None else None
+    except ValueError:
+        return None
+
+
+def gpu_processes(kfd_proc: Path = _KFD_PROCS) -> list[int] | None:
+    """PIDs with a GPU compute context (any GPU), or None when the KFD is not visible."""
+    try:
+        entries = list(kfd_proc.iterdir())
+    except OSError:
+        return None
+    return sorted(int(p.name) for p in entries if p.name.isdigit())
+
+
+def preflight(index: int = 0, *, strict: bool = True, kfd_proc: Path = _KFD_PROCS,
+              drm: Path | None = None) -> dict[str, Any]:
+    """Check that GPU ``index`` is idle before measuring.
+
+    Returns ``{"checked", "compute_apps", "utilization_gpu"}``; ``checked`` is
+    False when neither source is readable (a sandbox that hides sysfs). With
+    ``strict`` a busy card raises ``RuntimeError`` (the reference's behaviour);
+    otherwise the state is returned with ``"busy": True`` for the caller to
+    record next to its numbers.
+    """
+    devices = _gpu_device_dirs(drm if drm is not None else _DRM, "gpu_busy_percent")
+    used = _busy_percent(devices[index]) if index < len(devices) else None
+    pids = gpu_processes(kfd_proc)
+    mine = os.getpid()
+    foreign = [p for p in (pids or []) if p != mine]
+    state: dict[str, Any] = {"checked": used is not None or pids is not None,
+                             "compute_apps": foreign, "utilization_gpu": used}
+    problems = []
+    if foreign:
+        problems.append(f"other processes hold GPU contexts: {foreign}")
+    if used is not None and used >= BUSY_PERCENT:
+        problems.append(f"gpu_busy_percent = {used:.0f}% (want < {BUSY_PERCENT:.0f}%)")
+    state["busy"] = bool(problems)
+    if problems and strict:
+        raise RuntimeError("GPU is not idle: " + "; ".join(problems))
+    return state

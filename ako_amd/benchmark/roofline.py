@@ -222,7 +222,13 @@ def parse_copy_ceiling(text: str) -> dict[str, Any] | None:
             rows.append(json.loads(line))
     if not rows:
         return None
-    return max(rows, key=lambda r: r["gbps"])
+    best = dict(max(rows, key=lambda r: r["gbps"]))
+    timed_b2b = [r for r in rows if "b2b_gbps" in r]
+    if timed_b2b:
+        b2b = max(timed_b2b, key=lambda r: r["b2b_gbps"])
+        best["best_b2b_gbps"] = b2b["b2b_gbps"]
+        best["best_b2b_frac"] = b2b["b2b_frac"]
+    return best
 
 
 def copy_same_bytes(alg_bytes: int, *, timeout_s: float = 120.0) -> dict[str, Any] | None:

@@ -91,9 +91,17 @@ class CopyCeilings:
             self.seen[alg_bytes] = self.rf.copy_same_bytes(alg_bytes)
         return self.seen[alg_bytes]
 
-    def annotate(self, row: dict, gbps: float) -> None:
+    def annotate(self, row: dict, gbps: float, *, back_to_back: bool = False) -> None:
+        """Add the copy's share of peak and the kernel's rate over the copy's,
+        the copy timed the way the row was (per-launch events, or one event
+        pair around back-to-back launches)."""
         copy = self.get(row["alg_bytes"])
-        if copy is not None:
+        if copy is None:
+            return
+        if back_to_back and "best_b2b_gbps" in copy:
+            row["copy_pct_hbm_peak"] = round(100 * copy["best_b2b_frac"], 2)
+            row["kernel_over_copy"] = round(gbps / copy["best_b2b_gbps"], 4)
+        elif not back_to_back:
             row["copy_pct_hbm_peak"] = round(100 * copy["frac"], 2)
             row["kernel_over_copy"] = round(gbps / copy["gbps"], 4)
 
@@ -245,7 +253,7 @@ def time_extras(cells, torch, rf, peak, ceilings):
         row.pop("p50_us")
         row["copies"] = 1 if decode else len(fns)
         if nbytes >= STREAMING_BYTES:
-            ceilings.annotate(row, stats.gbps())
+            ceilings.annotate(row, stats.gbps(), back_to_back=True)
         if decode:
             # Median of five graph timings: one is under a millisecond of
             # device time, and clock changes move single readings by up to 15%.
@@ -370,6 +378,11 @@ def main() -> int:
     from ako_amd import _native
     from ako_amd.benchmark import roofline as rf
 
+    from ako_amd.benchmark.env import preflight, sample_env
+
+    idle = preflight(0, strict=False)  # recorded next to the numbers, not enforced
+    if idle["busy"]:
+        log(f"warning: the GPU is not idle before timing: {idle}")
     _native.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -486,6 +499,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "gpu_state": {"preflight": idle, "after": sample_env(0)},
         "selection": picked,
         "decoder": decoder,
         "rope_prefill": rope_prefill,

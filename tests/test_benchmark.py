@@ -228,10 +228,14 @@ def test_env_samples_degrade_to_none() -> None:
 
 def test_copy_ceiling_lines_pick_the_fastest_shape(monkeypatch, tmp_path) -> None:
     text = ("noise\n"
-            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 256, "us": 2.0, "gbps": 0.064, "frac": 0.1}\n'
-            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 1024, "us": 1.0, "gbps": 0.128, "frac": 0.2}\n')
+            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 256, "us": 2.0, "gbps": 0.064, "frac": 0.1, '
+            '"b2b_us": 1.0, "b2b_gbps": 0.128, "b2b_frac": 0.3}\n'
+            '{"bytes_per_buffer": 64, "traffic_bytes": 128, "block": 1024, "us": 1.0, "gbps": 0.128, "frac": 0.2, '
+            '"b2b_us": 1.5, "b2b_gbps": 0.085, "b2b_frac": 0.25}\n')
     best = rf.parse_copy_ceiling(text)
     assert best["block"] == 1024 and best["frac"] == 0.2
+    # The fastest back-to-back copy may be another shape: reported beside it.
+    assert best["best_b2b_frac"] == 0.3 and best["best_b2b_gbps"] == 0.128
     assert rf.parse_copy_ceiling("no json here") is None
     # Without the built probe the figure is simply absent.
     import ako_amd._build as build

@@ -255,3 +255,20 @@ def test_stack_on_hip_kernels_matches_hugging_face_llama(n_kv_heads: int) -> Non
             for t in range(9, 12):
                 got.append(stack(emb[:, t:t + 1], kv_cache=cache)[:, -1])
             torch.testing.assert_close(torch.stack(got, 1), want[:, 8:12], atol=2e-5, rtol=2e-5)
+
+
+def test_config5_workload_selection(tmp_path) -> None:
+    """The offline selection for the configs[4] decoder's shapes (prefill of
+    512 tokens and a decode step): every decision passes the gate, and the HIP
+    candidate is chosen for (nearly) every operation."""
+    from ako_amd.benchmark.optimize import config5_phases, optimize
+
+    doc = optimize(config5_phases(), device=torch.device(DEV), cache=KernelCache(path=tmp_path / "c.json"),
+                   warmup=3, repeats=10)
+    ops = doc["operations"]
+    assert len(ops) == 10 and "decode/rope_qk" in ops and "prefill/swiglu" in ops
+    hip = [name for name, op in ops.items() if op["backend"] == "hip"]
+    print({name: (op["selected_kernel"], op["speedup_vs_best_baseline"]) for name, op in ops.items()})
+    for op in ops.values():
+        assert op["source"] == "benchmark" and all(r["passed"] for r in op["ulp_reports"] if r["kernel"].endswith("_hip"))
+    assert len(hip) >= 9, hip

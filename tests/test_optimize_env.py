@@ -1,0 +1,85 @@
+"""Offline workload selection (``ako_amd.benchmark.optimize``) and the busy-GPU
+preflight (``ako_amd.benchmark.env.preflight``), on the CPU."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+import torch
+
+from ako_amd.benchmark import env
+from ako_amd.benchmark import optimize
+
+
+def _fake_sysfs(tmp_path, busy: str | None, pids: list[int] | None):
+    drm = tmp_path / "drm"
+    dev = drm / "card0" / "device"
+    dev.mkdir(parents=True)
+    if busy is not None:
+        (dev / "gpu_busy_percent").write_text(busy + "\n")
+    kfd = tmp_path / "kfd_proc"
+    if pids is not None:
+        kfd.mkdir()
+        for pid in pids:
+            (kfd / str(pid)).mkdir()
+    return drm, kfd
+
+
+def test_preflight_idle_card(tmp_path) -> None:
+    drm, kfd = _fake_sysfs(tmp_path, "0", [os.getpid()])
+    state = env.preflight(drm=drm, kfd_proc=kfd)
+    assert state == {"checked": True, "compute_apps": [], "utilization_gpu": 0.0, "busy": False}
+
+
+def test_preflight_refuses_a_busy_card(tmp_path) -> None:
+    drm, kfd = _fake_sysfs(tmp_path, "57", [os.getpid(), 4242])
+    with pytest.raises(RuntimeError, match="not idle.*4242.*57%"):
+        env.preflight(drm=drm, kfd_proc=kfd)
+    state = env.preflight(drm=drm, kfd_proc=kfd, strict=False)
+    assert state["busy"] and state["compute_apps"] == [4242] and state["utilization_gpu"] == 57.0
+    # Just under the threshold is idle.
+    drm2, kfd2 = _fake_sysfs(tmp_path / "b", "2", [])
+    assert env.preflight(drm=drm2, kfd_proc=kfd2)["busy"] is False
+
+
+def test_preflight_without_sysfs_is_unchecked(tmp_path) -> None:
+    state = env.preflight(drm=tmp_path / "none", kfd_proc=tmp_path / "none")
+    assert state == {"checked": False, "compute_apps": [], "utilization_gpu": None, "busy": False}
+
+
+def test_workload_tensors_follow_the_decoder_layer() -> None:
+    w = optimize.Workload(batch_size=2, seq_len=3, hidden_dim=64, num_heads=4, num_kv_heads=2, head_dim=16,
+                          ffn_dim=96, dtype=torch.float32)
+    t = w.tensors(torch.device("cpu"))
+    assert set(t) == {"rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"}
+    assert t["rmsnorm"][0][0].shape == (2, 3, 64) and t["rmsnorm"][0][1].shape == (64,)
+    q, k, cos, sin = t["rope_qk"][0]
+    assert q.shape == (2, 3, 4, 16) and k.shape == (2, 3, 2, 16) and cos.shape == (3, 8)
+    assert t["rope"][1] == {"style": "neox"} and t["swiglu"][0][0].shape == (2, 3, 96)
+    # Seeded: the same workload gives the same inputs.
+    assert torch.equal(t["rmsnorm"][0][0], w.tensors(torch.device("cpu"))["rmsnorm"][0][0])
+    phases = optimize.config5_phases()
+    assert phases["prefill"].seq_len == 512 and phases["decode"].seq_len == 1
+    assert phases["decode"].hidden_dim == 4096 and phases["decode"].ffn_dim == 11008
+
+
+def test_optimize_writes_the_selected_config(tmp_path) -> None:
+    """On the CPU the selector returns its default (only the baselines run
+    there); the document still has the reference's layout, one operation per
+    op, and the decisions are in the cache."""
+    out = tmp_path / "out"
+    rc = optimize.main(["--output-dir", str(out), "--device", "cpu", "--batch-size", "1", "--seq-len", "4",
+                        "--hidden-dim", "64", "--num-heads", "4", "--head-dim", "16", "--ffn-dim", "96",
+                        "--dtype", "fp32", "--cache-path", str(tmp_path / "c.json")])
+    assert rc == 0
+    doc = json.loads((out / "selected_config.json").read_text())
+    assert set(doc) == {"gpu", "compute_backend", "device", "created_at", "parameters", "operations", "cache"}
+    assert set(doc["operations"]) == {"rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"}
+    assert doc["parameters"]["hidden_dim"] == 64 and doc["parameters"]["dtype"] == "float32"
+    for op in doc["operations"].values():
+        assert op["source"] == "default" and op["selected_kernel"]
+    assert doc["compute_backend"] == "cpu"
+    lines = optimize.summary_lines(doc)
+    assert len(lines) == 5 and "[default]" in lines[0]
