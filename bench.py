@@ -15,7 +15,10 @@ Also reported on the same line:
                 per-launch duration from HIP events on the launch stream, and
                 a plain device copy of the same byte count timed the same way
                 (copy_same_bytes: the size's practical ceiling);
-  per_kernel    every launch of the step, each beside its copy ceiling;
+  per_kernel    every launch of the step, each beside its copy ceiling, by
+                per-launch events (as the roofline) and, under back_to_back,
+                on its own as 60 launches between one event pair over cold
+                input copies, beside a copy timed the same way;
   extras        the RoPE and SwiGLU cells, the
                 decode-size RMSNorm cells, the KV-cache RoPE and the
                 tensor-parallel RMSNorm halves; streaming cells beside their
@@ -135,6 +138,35 @@ def headline(args, torch, rf, dev, peak, rnd):
     del calls
     torch.cuda.empty_cache()
     return bytes_per_step, total_ms, per_launch
+
+
+def headline_back_to_back(torch, rf, dev, rnd) -> dict[str, float]:
+    """Each cell of the step on its own: mean ms per launch over 60 launches
+    queued back to back between one event pair, cycling through enough input
+    copies that every launch reads cold data (no per-launch events, whose
+    1.5-2 us would be counted in the launch); the median of three such runs."""
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+
+    out = {}
+    for dtype in (torch.float16, torch.bfloat16):
+        tag = "fp16" if dtype == torch.float16 else "bf16"
+        for h in RMS_HIDDEN:
+            w = rnd(h, dtype=dtype, scale=0.1, shift=1.0)
+            for residual in (False, True):
+                nbytes = (rf.alg_bytes_rmsnorm_residual(RMS_ROWS, h, dtype) if residual
+                          else rf.alg_bytes_rmsnorm(RMS_ROWS, h, dtype))
+                n = rf.copies_for_cold(nbytes, dev)
+                sets = [(rnd(RMS_ROWS, h, dtype=dtype), rnd(RMS_ROWS, h, dtype=dtype) if residual else None)
+                        for _ in range(n)]
+                fns = [(lambda x=x, r=r: rmsnorm_residual_hip(x, r, w, 1e-6)) if residual
+                       else (lambda x=x: rmsnorm_hip(x, w, 1e-6)) for x, r in sets]
+                for fn in fns:
+                    fn()
+                name = f"rmsnorm{'_residual' if residual else ''}_{tag}_{RMS_ROWS}x{h}"
+                out[name] = sorted(rf.time_back_to_back(fns, launches=60) for _ in range(3))[1]
+                del sets, fns
+                torch.cuda.empty_cache()
+    return out
 
 
 def extras_cells(torch, rf, dev, rnd):
@@ -398,10 +430,18 @@ def main() -> int:
     log(f"timed: {ms_per_step:.3f} ms/step, {value:.1f} GB/s ({100 * value / peak:.1f}% of {peak:.0f})")
     dominant = max(per_launch, key=lambda s: s.mean_ms)
     ceilings = CopyCeilings(rf)
+    b2b = headline_back_to_back(torch, rf, dev, rnd)
     per_kernel = []
     for stats in per_launch:
         row = stats.to_dict(peak)
         ceilings.annotate(row, stats.gbps())
+        ms = b2b.get(stats.name)
+        if ms:
+            alone = rf.LaunchStats(stats.name, stats.alg_bytes, [ms])
+            other = {"alg_bytes": stats.alg_bytes}
+            ceilings.annotate(other, alone.gbps(), back_to_back=True)
+            row["back_to_back"] = {"mean_us": round(ms * 1e3, 3), "pct_hbm_peak": round(100 * alone.gbps() / peak, 2),
+                                   **{k: v for k, v in other.items() if k != "alg_bytes"}}
         per_kernel.append(row)
 
     roofline = {
