@@ -265,10 +265,11 @@ def extras_cells(torch, rf, dev, rnd):
 
 def time_extras(cells, torch, rf, peak, ceilings):
     """Each cell: 60 back-to-back launches over its input copies between one
-    event pair (per-launch events would distort 5-30 us kernels); streaming
-    cells beside the copy of the same bytes; decode cells also as device time
-    per call from replayed HIP graphs, inputs hot (64 calls on one input) and
-    cold (64 calls on 64 inputs after an eviction pass)."""
+    event pair (per-launch events would distort 5-30 us kernels; streaming
+    cells take the median of three such timings) beside the copy of the same
+    bytes; decode cells also as device time per call from replayed HIP graphs,
+    inputs hot (64 calls on one input) and cold (64 calls on 64 inputs after
+    an eviction pass)."""
     extras = []
     for _, _, fns, _ in cells:
         for fn in fns[:2]:
@@ -278,7 +279,9 @@ def time_extras(cells, torch, rf, peak, ceilings):
         if decode:
             ms = rf.time_back_to_back(fns[:1], launches=60)  # hot: one input, as before
         else:
-            ms = rf.time_back_to_back(fns, launches=60)
+            # Median of three: single 60-launch timings of these 8-220 us
+            # launches move by several percent from one to the next.
+            ms = sorted(rf.time_back_to_back(fns, launches=60) for _ in range(3))[1]
         stats = rf.LaunchStats(name, nbytes, [ms])
         row = stats.to_dict(peak)
         row.pop("launches")
