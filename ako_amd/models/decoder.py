@@ -163,8 +163,10 @@ class StaticKVCache:
         self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
         self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
+        #: Host-side mirror of ``pos``: advanced by every eagerly run step (the
+        #: replays of a captured step advance only the device copy, and
+        #: ``GraphedGreedy`` sets the mirror after its replays).
         self.host_len = 0
-        self.slots = torch.arange(max_len, device=device)
         self.mask = torch.zeros(1, 1, 1, max_len, dtype=dtype, device=device)
 
     @property
@@ -174,6 +176,8 @@ class StaticKVCache:
     def set_length(self, length: int) -> None:
         """Host-side: the first ``length`` slots are filled (after a prefill).
         Sets ``pos`` and the mask: 0 for filled slots, -inf beyond."""
+        if length > self.max_len:
+            raise ValueError(f"KV cache overflow: {length} > max_len {self.max_len}")
         self.host_len = length
         self.pos.fill_(length)
         self.mask.fill_(float("-inf"))
@@ -182,11 +186,15 @@ class StaticKVCache:
     def begin_step(self) -> None:
         """Open slot ``pos`` in the attention mask for the token being decoded:
         one device-side write per step (capturable). Slots below ``pos`` were
-        opened by earlier steps or by ``set_length``."""
+        opened by earlier steps or by ``set_length``. A step past the last slot
+        is refused on the host: the device-side index would be out of range."""
+        if self.host_len >= self.max_len:
+            raise ValueError(f"KV cache overflow: decode step at slot {self.host_len} of {self.max_len}")
         self.mask.index_fill_(-1, self.pos, 0.0)
 
     def end_step(self, tokens: int) -> None:
         self.pos.add_(tokens)
+        self.host_len += tokens
 
     def rope_rows(self, cos_full: torch.Tensor, sin_full: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         return cos_full.index_select(0, self.pos), sin_full.index_select(0, self.pos)
@@ -503,12 +511,15 @@ class GraphedGreedy:
         with torch.cuda.stream(side):
             self._step()
             self.cache.pos.sub_(1)  # undo the warmup step: position and token
+            self.cache.host_len -= 1
             self.ids.copy_(first)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._step()
+        self.cache.host_len -= 1  # capture ran no step on the device
+        self._ran = False
 
     def _step(self) -> None:
         logits = self.model.logits_last(self.ids, self.cache)
@@ -518,8 +529,15 @@ class GraphedGreedy:
 
     @torch.no_grad()
     def run(self) -> torch.Tensor:
+        """Replay the captured step ``steps - 1`` times; once per runner, since
+        each replay advances the cache position and the slab holds exactly
+        ``prompt + steps`` slots."""
+        if self._ran:
+            raise RuntimeError("GraphedGreedy.run() decodes once; build a new runner for another pass")
+        self._ran = True
         for _ in range(self.steps - 1):
             self.graph.replay()
+        self.cache.host_len = self.prompt_len + self.steps - 1
         return self.history.view(1, -1)
 
 

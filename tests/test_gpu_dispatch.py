@@ -183,9 +183,13 @@ def test_graphed_greedy_matches_eager_static_decoding(n_kv_heads: int) -> None:
                 eager.append(ids)
             eager_tokens = torch.cat(eager, 1)
             for _ in range(2):  # two independent runners: every replay must reproduce eager
-                graphed = GraphedGreedy(model, prompt, 12).run()
+                runner = GraphedGreedy(model, prompt, 12)
+                graphed = runner.run()
                 torch.cuda.synchronize()
                 assert torch.equal(graphed, eager_tokens), (backend, graphed, eager_tokens)
+                assert runner.cache.length == 17 + 11
+                with pytest.raises(RuntimeError, match="decodes once"):
+                    runner.run()  # a second pass would step past the slab
 
 
 def test_torch_binding_matches_the_ctypes_path() -> None:

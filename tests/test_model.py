@@ -89,9 +89,31 @@ def test_static_cache_decode_matches_cat_cache() -> None:
             b = model.logits_last(ids, static)
             assert_close(b, a, atol=1e-5, rtol=1e-5)
             ids = a.argmax(-1, keepdim=True)
-    assert int(static.pos) == 12 and static.length == 7
+    # The host mirror follows the decode steps, so a later multi-token call
+    # starts at the true length.
+    assert int(static.pos) == 12 and static.length == 12
     with pytest.raises(ValueError, match="overflow"):
         static.update(0, torch.zeros(1, 20, 2, 16), torch.zeros(1, 20, 2, 16))
+
+
+def test_static_cache_refuses_steps_past_its_slab() -> None:
+    """A decode step past the last slot raises on the host before any
+    device-side index (the mask slot, the cache slot) could go out of range."""
+    cfg = ModelConfig(hidden_dim=64, n_layers=1, n_heads=4, n_kv_heads=4, intermediate_dim=96,
+                      max_seq_len=16, vocab_size=50, eps=1e-6)
+    model = build_lm(cfg, backend="ako", dtype=torch.float32, seed=6)
+    prompt = torch.randint(0, 50, (1, 5), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        static = model.stack.new_static_cache(7)
+        ids = model.logits_last(prompt, static).argmax(-1, keepdim=True)
+        for _ in range(2):  # slots 5 and 6
+            ids = model.logits_last(ids, static).argmax(-1, keepdim=True)
+        assert static.length == 7 and int(static.pos) == 7
+        with pytest.raises(ValueError, match="overflow"):
+            model.logits_last(ids, static)
+        assert int(static.pos) == 7  # nothing ran
+        with pytest.raises(ValueError, match="overflow"):
+            model.stack.new_static_cache(4).set_length(5)
 
 
 def _hf_pair(n_kv_heads: int):
