@@ -19,8 +19,9 @@ every call reads inputs that at least that much traffic has passed over since
 they were last touched: cold, with nothing added to the timed region and
 nothing subtracted. Inputs that large on their own need no copies. Very small
 inputs would need tens of thousands of copies, so the ring is capped at
-``MAX_RING_COPIES``; ``l2_state`` then records what the ring does reach
-(``"cold"``, ``"l2-cold"`` when it covers only the L2s, or ``"warm"``).
+``MAX_RING_COPIES`` (and at a quarter of the free device memory);
+``l2_state`` then records what the ring does reach (``"cold"``,
+``"l2-cold"`` when it covers only the L2s, or ``"warm"``).
 
 Graph mode captures one pass over (up to ``GRAPH_RING_CALLS`` entries of) the
 ring into a single HIP graph and times replays, which removes the host launch
@@ -227,8 +228,18 @@ def _tensor_bytes(args: tuple[Any, ...]) -> int:
     return sum(a.numel() * a.element_size() for a in args if isinstance(a, torch.Tensor))
 
 
+#: Share of the device's free memory a ring may take (first-sight selection in
+#: a serving process must not be the allocation that runs it out of memory).
+RING_FREE_SHARE = 0.25
+
+
 def plan_ring(args: tuple[Any, ...], device: torch.device, cold: bool) -> tuple[int, str]:
-    """``(copies, l2_state)`` of the rotation that makes calls read cold inputs."""
+    """``(copies, l2_state)`` of the rotation that makes calls read cold inputs.
+
+    The ring wants 2 x (L2 + MALL) bytes, holds at most ``MAX_RING_COPIES``
+    copies and never more than ``RING_FREE_SHARE`` of the free device memory;
+    ``l2_state`` says what the ring it gets can reach.
+    """
     l2, mall = cache_bytes(device)
     if device.type != "cuda":
         return 1, "n/a"
@@ -237,6 +248,9 @@ def plan_ring(args: tuple[Any, ...], device: torch.device, cold: bool) -> tuple[
     per_call = max(1, _tensor_bytes(args))
     want = 2 * (l2 + mall)
     copies = min(MAX_RING_COPIES, max(1, math.ceil(want / per_call)))
+    if copies > 1:
+        free, _ = torch.cuda.mem_get_info(device)
+        copies = max(1, min(copies, int(RING_FREE_SHARE * free) // per_call))
     return copies, ring_state(copies * per_call, l2, mall)
 
 

@@ -255,3 +255,24 @@ def test_bench_refuses_more_than_one_gpu() -> None:
                          timeout=120)
     assert out.returncode == 2
     assert "measures one GPU" in out.stderr and out.stdout == ""
+
+
+def test_ring_plan_covers_the_caches_within_free_memory(monkeypatch) -> None:
+    """On a GPU the ring wants 2 x (L2 + MALL) bytes of copies; it is capped
+    at MAX_RING_COPIES and at a quarter of the free device memory, and its
+    l2_state says what it reaches (device queries faked, no GPU needed)."""
+    from ako_amd.benchmark import bench_op as bo
+
+    l2, mall = 32 << 20, 256 << 20
+    monkeypatch.setattr(bo, "cache_bytes", lambda device: (l2, mall))
+    gpu = torch.device("cuda", 0)
+    x = torch.empty(4 << 20, dtype=torch.int8)  # 4 MiB per call
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (64 << 30, 288 << 30))
+    assert bo.plan_ring((x,), gpu, cold=True) == (144, "cold")  # 576 MiB / 4 MiB
+    assert bo.plan_ring((x,), gpu, cold=False) == (1, "warm")
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (512 << 20, 288 << 30))
+    assert bo.plan_ring((x,), gpu, cold=True) == (32, "l2-cold")  # 128 MiB: a quarter of 512 MiB
+    tiny = torch.empty(64, dtype=torch.int8)
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (64 << 30, 288 << 30))
+    assert bo.plan_ring((tiny,), gpu, cold=True) == (bo.MAX_RING_COPIES, "warm")
+    assert bo.plan_ring((x,), torch.device("cpu"), cold=True) == (1, "n/a")
