@@ -261,8 +261,9 @@ def test_ring_plan_covers_the_caches_within_free_memory(monkeypatch) -> None:
     """On a GPU the ring wants 2 x (L2 + MALL) bytes of copies; it is capped
     at MAX_RING_COPIES and at a quarter of the free device memory, and its
     l2_state says what it reaches (device queries faked, no GPU needed)."""
-    from ako_amd.benchmark import bench_op as bo
+    import importlib
 
+    bo = importlib.import_module("ako_amd.benchmark.bench_op")  # the module, not the function
     l2, mall = 32 << 20, 256 << 20
     monkeypatch.setattr(bo, "cache_bytes", lambda device: (l2, mall))
     gpu = torch.device("cuda", 0)
