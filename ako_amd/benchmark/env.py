@@ -135,3 +135,63 @@ def preflight(index: int = 0, *, strict: bool = True, kfd_proc: Path = _KFD_PROC
     if problems and strict:
         raise RuntimeError("GPU is not idle: " + "; ".join(problems))
     return state
+
+
+def report() -> dict[str, Any]:
+    """What ``python -m ako_amd.benchmark.env`` prints: the runtime, the device,
+    whether the HIP library and its binding load, and whether the GPU is idle
+    (the reference's ``scripts/check_environment.py``, ROCm-side)."""
+    import sys
+
+    import torch
+
+    from ako_amd import _native
+    from ako_amd.dispatcher.hardware import get_device_info
+
+    info = get_device_info()
+    out: dict[str, Any] = {
+        "python": sys.version.split()[0],
+        "torch": torch.__version__,
+        "hip_runtime": getattr(torch.version, "hip", None),
+        "gpu_available": torch.cuda.is_available(),
+        "compute_backend": info.compute_backend,
+        "device": info.device_name,
+        "cache_key": info.cache_key,
+        "driver": info.driver_version,
+        "host": host_cpu(),
+    }
+    try:
+        lib = _native.load()
+        out["hip_library"] = lib.ako_build_info().decode()
+    except _native.HipLibraryError as exc:
+        out["hip_library"] = f"not loadable: {exc}"
+    try:
+        out["torch_binding"] = _native.torch_binding() is not None
+    except _native.HipLibraryError:
+        out["torch_binding"] = False
+    if torch.cuda.is_available():
+        out["preflight"] = preflight(torch.cuda.current_device(), strict=False)
+        out["gpu_state"] = sample_env(torch.cuda.current_device())
+    return out
+
+
+def main(argv: list[str] | None = None) -> int:
+    import json
+
+    state = report()
+    width = max(len(k) for k in state)
+    for key, value in state.items():
+        shown = json.dumps(value) if isinstance(value, (dict, list)) else str(value)
+        print(f"{key:<{width}}  {shown}")
+    if not state["gpu_available"]:
+        print("\nCPU only: the oracle, the gate, the selector and the ABI checks run here "
+              "(pytest -m 'not gpu'); the HIP kernels need an MI355X (gfx950).")
+    elif str(state["hip_library"]).startswith("not loadable"):
+        print("\nThe GPU is visible but the kernel library is not built: "
+              "python -c 'import __graft_entry__ as g; g.build()'")
+        return 1
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -83,3 +83,15 @@ def test_optimize_writes_the_selected_config(tmp_path) -> None:
     assert doc["compute_backend"] == "cpu"
     lines = optimize.summary_lines(doc)
     assert len(lines) == 5 and "[default]" in lines[0]
+
+
+def test_environment_report_on_the_cpu(capsys) -> None:
+    """The ``check_environment`` equivalent: runtime versions, device, whether
+    the library and binding load; exit 0 on a CPU-only machine."""
+    state = env.report()
+    assert state["torch"] == torch.__version__ and state["gpu_available"] is False
+    assert state["compute_backend"] == "cpu" and state["cache_key"] == "cpu_-1"
+    assert "arch=gfx950" in state["hip_library"] or state["hip_library"].startswith("not loadable")
+    assert env.main([]) == 0
+    out = capsys.readouterr().out
+    assert "hip_library" in out and "CPU only" in out
