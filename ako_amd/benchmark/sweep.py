@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import sys
 from pathlib import Path
 from typing import Any, Callable, Iterator
@@ -110,6 +111,7 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
     reports: dict[str, BenchmarkReport] = {}
     wins = total = decode_total = decode_wins = 0
     others: list[dict[str, Any]] = []
+    leads: dict[str, list[float]] = {}
     for op, shape, dtype, tensors, kw in cells(ops, device):
         if keep is not None and not keep(op, shape, dtype):
             continue
@@ -145,6 +147,9 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
         if not hip_won:
             others.append({"cell": cell_name(op, shape, dtype), "selected": result.entry.kernel_name,
                            "latencies_us": {k: round(v * 1e3, 2) for k, v in lat.items()}})
+        if result.speedup_vs_best_baseline:
+            phase = "decode" if is_decode(op, shape) else "prefill"
+            leads.setdefault(f"{op}_{phase}", []).append(result.speedup_vs_best_baseline)
         if not quiet:
             print(f"[sweep] {op:17s} {str(shape):22s} {str(dtype)[6:]:9s} -> {result.entry.kernel_name:22s} "
                   + " ".join(f"{k}={v * 1e3:.1f}us" for k, v in lat.items()), flush=True)
@@ -156,6 +161,9 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
         save_report(report, out_dir / f"selection_{op}.json")
     summary = {"cells": total, "hip_selected": wins, "hip_win_rate": round(wins / total, 4) if total else None,
                "decode_cells": decode_total, "decode_hip_selected": decode_wins,
+               # The reference campaign's headline numbers (scripts/run_campaign.py:287-337):
+               # the selected kernel's median lead over the fastest baseline, per op and phase.
+               "median_lead_vs_best_baseline": {k: round(statistics.median(v), 3) for k, v in sorted(leads.items())},
                "not_hip": others, "gpu": info.device_name, "cache_key": info.cache_key}
     (out_dir / "selection_summary.json").write_text(json.dumps(summary, indent=2))
     return summary
