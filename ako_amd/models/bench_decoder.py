@@ -67,9 +67,10 @@ def graphed_step_breakdown(model, prompt: torch.Tensor, steps: int = 32) -> dict
 
 def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3,
                 device: str = "cuda", seed: int = 0, graphed: bool = True, prefill_warmup: int = 3,
-                prefill_repeats: int = 20, breakdown: bool = False) -> dict[str, Any]:
+                prefill_repeats: int = 20, breakdown: bool = False, fused_qkv: bool = True) -> dict[str, Any]:
     cfg = config5()
     cfg.max_seq_len = prompt_len + decode_steps
+    cfg.fused_qkv = fused_qkv
     model = build_lm(cfg, backend=backend, device=device, dtype=torch.float16, seed=seed)
     gen = torch.Generator(device="cpu").manual_seed(seed)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=gen).to(device)
@@ -131,9 +132,12 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
     }
 
 
-def compare(prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3) -> dict[str, Any]:
+def compare(prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3,
+            fused_qkv: bool = True) -> dict[str, Any]:
+    """Both backends on the same weights and the same projection layout: the
+    difference between them is the four operations' kernels alone."""
     results = {b: run_config5(b, prompt_len=prompt_len, decode_steps=decode_steps, repeats=repeats,
-                              breakdown=(b == "ako"))
+                              breakdown=(b == "ako"), fused_qkv=fused_qkv)
                for b in ("torch", "ako")}
     ta, tt = results["ako"]["tokens"], results["torch"]["tokens"]
     first_diff = next((i for i, (a, b) in enumerate(zip(ta, tt)) if a != b), None)
@@ -141,6 +145,7 @@ def compare(prompt_len: int = 512, decode_steps: int = 128, repeats: int = 3) ->
         r.pop("tokens")
     return {
         "config": "configs[4]: 4 layers, hidden 4096, 32x128 heads, FFN 11008, fp16, vocab 32000, MHA",
+        "qkv_projection": "fused" if fused_qkv else "separate",
         "torch": results["torch"],
         "ako": results["ako"],
         "prefill_speedup": round(results["torch"]["prefill_ms"] / results["ako"]["prefill_ms"], 3),
@@ -160,15 +165,18 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--repeats", type=int, default=3)
     ap.add_argument("--backend", choices=("torch", "ako"), default=None,
                     help="run one backend only (e.g. under a profiler) instead of comparing both")
+    ap.add_argument("--separate-qkv", action="store_true",
+                    help="three q/k/v projections (the reference's layout) instead of one fused GEMM")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("configs[4] needs a GPU", file=sys.stderr)
         return 1
     if args.backend:
-        out = run_config5(args.backend, prompt_len=args.prompt, decode_steps=args.steps, repeats=args.repeats)
+        out = run_config5(args.backend, prompt_len=args.prompt, decode_steps=args.steps, repeats=args.repeats,
+                          fused_qkv=not args.separate_qkv)
         out.pop("tokens")
     else:
-        out = compare(args.prompt, args.steps, args.repeats)
+        out = compare(args.prompt, args.steps, args.repeats, fused_qkv=not args.separate_qkv)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -241,13 +241,16 @@ def test_torch_binding_matches_the_ctypes_path() -> None:
     assert torch.equal(y_side, rm.rmsnorm_hip_ctypes(x, w, 1e-6))
 
 
+@pytest.mark.parametrize("fused_qkv", [True, False])
 @pytest.mark.parametrize("n_kv_heads", [4, 2])
-def test_stack_on_hip_kernels_matches_hugging_face_llama(n_kv_heads: int) -> None:
+def test_stack_on_hip_kernels_matches_hugging_face_llama(n_kv_heads: int, fused_qkv: bool) -> None:
     """The decoder with the HIP kernels (fp32) against Hugging Face's LlamaModel
-    carrying the same weights, prompt and cached decoding, on the GPU."""
+    carrying the same weights, prompt and cached decoding, on the GPU. With the
+    fused projection q, k and v reach the RoPE kernels as strided column
+    slices of one GEMM output; without it, as contiguous tensors."""
     from tests.test_model import _hf_pair
 
-    hf, stacks = _hf_pair(n_kv_heads)
+    hf, stacks = _hf_pair(n_kv_heads, fused_qkv)
     hf, stack = hf.to(DEV), stacks["ako"].to(DEV)
     ids = torch.randint(0, 50, (1, 12), generator=torch.Generator().manual_seed(2)).to(DEV)
     with torch.no_grad():

@@ -116,7 +116,7 @@ def test_static_cache_refuses_steps_past_its_slab() -> None:
             model.stack.new_static_cache(4).set_length(5)
 
 
-def _hf_pair(n_kv_heads: int):
+def _hf_pair(n_kv_heads: int, fused_qkv: bool = True):
     """A small Hugging Face LlamaModel (random weights, built offline from a
     config) and this package's stack carrying the same weights."""
     transformers = pytest.importorskip("transformers")
@@ -132,14 +132,15 @@ def _hf_pair(n_kv_heads: int):
         for p in hf.parameters():
             p.normal_(0.0, 0.05)
     cfg = ModelConfig(hidden_dim=64, n_layers=2, n_heads=4, n_kv_heads=n_kv_heads, intermediate_dim=96,
-                      max_seq_len=64, vocab_size=50, eps=1e-6, rope_base=10000.0)
+                      max_seq_len=64, vocab_size=50, eps=1e-6, rope_base=10000.0, fused_qkv=fused_qkv)
     stacks = {}
     for backend in ("torch", "ako"):
         stack = DecoderStack(cfg, backend).eval()
         with torch.no_grad():
             for ours, theirs in zip(stack.layers, hf.layers):
-                for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
-                    getattr(ours.attention, name).weight.copy_(getattr(theirs.self_attn, name).weight)
+                att = theirs.self_attn
+                ours.attention.load_qkv(att.q_proj.weight, att.k_proj.weight, att.v_proj.weight)
+                ours.attention.o_proj.weight.copy_(att.o_proj.weight)
                 for name in ("gate_proj", "up_proj", "down_proj"):
                     getattr(ours.mlp, name).weight.copy_(getattr(theirs.mlp, name).weight)
                 ours.input_norm_weight.copy_(theirs.input_layernorm.weight)
@@ -149,12 +150,14 @@ def _hf_pair(n_kv_heads: int):
     return hf, stacks
 
 
+@pytest.mark.parametrize("fused_qkv", [True, False])
 @pytest.mark.parametrize("n_kv_heads", [4, 2])
-def test_stack_matches_hugging_face_llama(n_kv_heads: int) -> None:
+def test_stack_matches_hugging_face_llama(n_kv_heads: int, fused_qkv: bool) -> None:
     """An independent implementation of the same architecture (the reference's
     tests/test_hf_loader.py compares against it too): hidden states of a
-    prompt, and token-by-token decoding through the KV caches, within 1e-5."""
-    hf, stacks = _hf_pair(n_kv_heads)
+    prompt, and token-by-token decoding through the KV caches, within 1e-5,
+    with the q/k/v projections fused into one GEMM or kept as three."""
+    hf, stacks = _hf_pair(n_kv_heads, fused_qkv)
     ids = torch.randint(0, 50, (1, 12), generator=torch.Generator().manual_seed(1))
     with torch.no_grad():
         want = hf(input_ids=ids).last_hidden_state
