@@ -153,6 +153,16 @@ int ako_set_tuning(int op, int key, int value) {
         ako::g_rms_tuning.early_weights = value;
         return AKO_OK;
       }
+      if (key == 9) {
+        if (value > 2) return fail(AKO_ERR_INVALID_ARGUMENT, "pipeline must be 0, 1 or 2");
+        ako::g_rms_tuning.pipeline = value;
+        return AKO_OK;
+      }
+      if (key == 10) {
+        if (value > 32) return fail(AKO_ERR_INVALID_ARGUMENT, "pipelined workgroups per CU above 32");
+        ako::g_rms_tuning.pipe_blocks_per_cu = value;
+        return AKO_OK;
+      }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

@@ -23,6 +23,8 @@ struct RmsTuning {
   int xcd_chunk = 0;        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
   int max_blocks = 0;       // key 7: cap on workgroups per launch (0 = 2^31 work-items)
   int early_weights = 0;    // key 8: 1 = weights after the row's loads return, 2 = with them (0 = by launch size)
+  int pipeline = 0;         // key 9: 1 = never the pipelined persistent kernel, 2 = whenever eligible (0 = heuristic)
+  int pipe_blocks_per_cu = 0;  // key 10: workgroups per CU in the pipelined grid (0 = 16 wavefronts per CU)
 };
 struct RopeTuning {
   int tokens_per_block = 0;  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)

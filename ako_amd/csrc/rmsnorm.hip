@@ -1,6 +1,6 @@
 // RMSNorm and residual-add + RMSNorm for gfx950.
 //
-// Two kernels:
+// Three kernels:
 //
 // rmsnorm_reg  - the row lives in registers. A row is owned by WPR wavefronts
 //   (64 * WPR lanes); lane t of the row holds the 16-byte packets
@@ -16,6 +16,11 @@
 //   group instead of once per packet. Wide rows are handed to the 8 XCDs in
 //   runs of consecutive rows (block_order) rather than row by row.
 //
+// rmsnorm_pipe - rmsnorm_reg's row layout in a persistent, software-pipelined
+//   grid: each workgroup walks a sequence of rows and issues the next row's
+//   loads before it reduces and writes the current one. Taken by launches of
+//   many full rows of at most 16 KiB of input at one packet per lane.
+//
 // rmsnorm_stream - any width, any alignment (E = 1 scalar packets when the
 //   rows are not 16-byte aligned). One 256-lane workgroup per row, two passes
 //   over global memory: the first accumulates the sum of squares (and writes
@@ -29,6 +34,9 @@
 //   y    = to_T((x * rstd) * w)      (two rounded fp32 multiplies, this order)
 // and for the residual variant s = to_T(x + r) is normalised, as the
 // reference adds in the storage dtype before normalising.
+
+#include <algorithm>
+#include <atomic>
 
 #include "common.h"
 #include "launch.h"
@@ -201,6 +209,137 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     }
   }
   if (has_tail) yr[tcol] = from_f32<T>((to_f32(vt) * rstd) * to_f32(w[tcol]));
+}
+
+// rmsnorm_pipe - rmsnorm_reg's row layout (WPR wavefronts per row, lane t
+// holding packets t + k * 64 * WPR) in a persistent grid: a workgroup owns one
+// row at a time and walks a sequence of rows, and it issues the loads of its
+// next row before it reduces and writes the current one. In rmsnorm_reg a
+// workgroup reads its row, waits, then only writes, so a CU's reads stall
+// while its rows drain; here every wavefront keeps one row's reads in flight
+// through its writes. The lane's slice of the weight row is the same for
+// every row and is loaded once. Only full rows take this kernel
+// (hidden = 64 * WPR * VPT * E), so every load is unconditional. The
+// arithmetic and the order of every sum are rmsnorm_reg's, so the two
+// kernels give bitwise-identical outputs.
+//
+// The loop holds two register buffers, A and B, and is unrolled by two with
+// the first row peeled off, so that both ways into the loop head leave the
+// same operations outstanding (B's loads, then one row's stores). The
+// compiler's wait counts are then exact: consuming a buffer waits for that
+// buffer's loads only, not for the stores issued after them (vmcnt counts
+// loads and stores in one in-order queue on gfx950).
+//
+// Row sequence: with xcd_runs the rows are cut into 8 contiguous ranges, one
+// per XCD (workgroup b runs on XCD b % 8; the grid is a multiple of 8), and
+// the workgroups of one XCD interleave within its range; otherwise the grid
+// strides over all rows.
+template <typename T, int E, int VPT, int TPR, bool RES>
+__device__ __forceinline__ void pipe_load(const T* __restrict__ xr, const T* __restrict__ rr, int t,
+                                          Pack<T, E> (&vx)[VPT], Pack<T, E> (&vr)[VPT]) {
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    vx[k] = load_pack<T, E, true>(xr + (t + k * TPR) * E);
+    if constexpr (RES) vr[k] = load_pack<T, E, true>(rr + (t + k * TPR) * E);
+  }
+}
+
+template <typename T, typename W, int E, int VPT, int WPR, bool RES, int SLOT>
+__device__ __forceinline__ void pipe_row(Pack<T, E> (&vx)[VPT], const Pack<T, E> (&vr)[VPT],
+                                         const WeightPacket<W, E> (&wv)[VPT], float (&partial)[2][WPR],
+                                         T* __restrict__ y, T* __restrict__ rout, int64_t row, int64_t sy,
+                                         int64_t srout, int t, float inv_h, float eps) {
+  constexpr int TPR = kWave * WPR;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    if constexpr (RES) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) vx[k].e[e] = from_f32<T>(to_f32(vx[k].e[e]) + to_f32(vr[k].e[e]));
+      store_pack<T, E, true>(rout + row * srout + (t + k * TPR) * E, vx[k]);
+    }
+    ss = sumsq_add(vx[k], ss);
+  }
+  ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    // Rows alternate between two slots: a wavefront one row ahead writes the
+    // other slot, and cannot get two rows ahead without passing this barrier.
+    if (lane == 0) partial[SLOT][wave] = ss;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < WPR; ++j) ss += partial[SLOT][j];
+  }
+  const float rstd = rsqrtf(ss * inv_h + eps);
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    Pack<T, E> o;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o.e[e] = from_f32<T>((to_f32(vx[k].e[e]) * rstd) * wv[k][e]);
+    store_pack<T, E, true>(y + row * sy + (t + k * TPR) * E, o);
+  }
+}
+
+template <typename T, typename W, int WPR, int VPT, bool RES>
+__global__ __launch_bounds__(kWave* WPR) void rmsnorm_pipe(
+    const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
+    T* __restrict__ y, T* __restrict__ rout, int64_t rows, int64_t sx, int64_t sr, int64_t sy,
+    int64_t srout, float inv_h, float eps, int xcd_runs) {
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  constexpr int TPR = kWave * WPR;
+  using P = Pack<T, E>;
+  const int t = threadIdx.x;
+
+  int64_t row, step, end;
+  if (xcd_runs) {
+    const int64_t xcd = blockIdx.x % 8, per_xcd = gridDim.x / 8;
+    row = xcd * rows / 8 + blockIdx.x / 8;
+    end = (xcd + 1) * rows / 8;
+    step = per_xcd;
+  } else {
+    row = blockIdx.x;
+    end = rows;
+    step = gridDim.x;
+  }
+  if (row >= end) return;  // the whole workgroup: no barrier is reached
+  // Rows of this workgroup: row + i * step for i < n (n < 2^31: the launcher
+  // sends no more rows). The prefetch after the last row reads the weight
+  // row instead (L2-resident, at least as long as one row of x, discarded),
+  // so that every load is issued unconditionally.
+  const int n = static_cast<int>((end - row + step - 1) / step);
+  const T* spare = reinterpret_cast<const T*>(w);
+
+  WeightPacket<W, E> wv[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) wv[k].load(w + (t + k * TPR) * E);
+  __shared__ float partial[2][WPR];
+
+  P ax[VPT], bx[VPT];
+  [[maybe_unused]] P ar[VPT];
+  [[maybe_unused]] P br[VPT];
+  pipe_load<T, E, VPT, TPR, RES>(x + row * sx, res + row * sr, t, ax, ar);
+  const bool two = n > 1;
+  pipe_load<T, E, VPT, TPR, RES>(two ? x + (row + step) * sx : spare, two ? res + (row + step) * sr : spare, t, bx,
+                                 br);
+  pipe_row<T, W, E, VPT, WPR, RES, 0>(ax, ar, wv, partial, y, rout, row, sy, srout, t, inv_h, eps);
+  int i = 1;
+  for (; i + 1 < n; i += 2) {
+    // Rows i (in B) and i + 1 exist; A takes row i + 1, then B row i + 2.
+    const int64_t r = row + static_cast<int64_t>(i) * step;
+    pipe_load<T, E, VPT, TPR, RES>(x + (r + step) * sx, res + (r + step) * sr, t, ax, ar);
+    pipe_row<T, W, E, VPT, WPR, RES, 1>(bx, br, wv, partial, y, rout, r, sy, srout, t, inv_h, eps);
+    const bool more = i + 2 < n;
+    pipe_load<T, E, VPT, TPR, RES>(more ? x + (r + 2 * step) * sx : spare,
+                                   more ? res + (r + 2 * step) * sr : spare, t, bx, br);
+    pipe_row<T, W, E, VPT, WPR, RES, 0>(ax, ar, wv, partial, y, rout, r + step, sy, srout, t, inv_h, eps);
+  }
+  if (i < n)  // the last row, in B
+    pipe_row<T, W, E, VPT, WPR, RES, 1>(bx, br, wv, partial, y, rout, row + static_cast<int64_t>(i) * step, sy,
+                                        srout, t, inv_h, eps);
 }
 
 // Two-pass kernel: one workgroup of kStreamBlock lanes per row, packets of E
@@ -511,6 +650,73 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   return run_reg_launch<T, W, WPR, VPT, RES, false>(a, stream);
 }
 
+// Compute units of the current device (the pipelined grid's size), read
+// once per device.
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Widest input row (x, plus the residual) the pipelined kernel takes by
+// default, and the fewest rows per workgroup at which plain rows take it.
+constexpr int64_t kPipeMaxRowBytes = 16 * 1024;
+constexpr int64_t kPipeMinRowsPerBlock = 16;
+
+// Shapes with a pipelined instantiation (the defaults of launches of many
+// rows up to 65536 half-precision elements, and their neighbours).
+constexpr RegShape kPipeShapes[] = {{4, 2}, {8, 1}, {8, 2}, {16, 1}, {16, 2}, {16, 4}};
+
+bool pipe_shape(const RegShape& s) {
+  for (const RegShape& c : kPipeShapes)
+    if (c.wpr == s.wpr && c.vpt == s.vpt) return true;
+  return false;
+}
+
+// Workgroups of a pipelined launch (a multiple of 8). Workgroups per CU: 16
+// wavefronts per CU for plain rows, 8 for residual rows (two tensors in
+// flight per row). Measured at 16384 rows of 4096 half elements: plain 6598
+// GB/s with 16 wavefronts per CU against 6029 with 8; residual 6976 with 8
+// against 6826 with 16.
+int64_t pipe_blocks(int wpr, bool residual, int64_t rows) {
+  const int64_t per_cu = g_rms_tuning.pipe_blocks_per_cu > 0 ? g_rms_tuning.pipe_blocks_per_cu
+                                                             : std::max(1, (residual ? 8 : 16) / wpr);
+  const int64_t blocks = std::min<int64_t>(rows, per_cu * device_cus());
+  return std::max<int64_t>(8, blocks / 8 * 8);
+}
+
+template <typename T, typename W, int WPR, int VPT, bool RES>
+hipError_t run_pipe(const RmsArgs& a, hipStream_t stream) {
+  const int64_t blocks = pipe_blocks(WPR, RES, a.rows);
+  const int xcd_runs = g_rms_tuning.row_order == 1 ? 0 : 1;
+  hipLaunchKernelGGL((rmsnorm_pipe<T, W, WPR, VPT, RES>), dim3(static_cast<unsigned>(blocks)), dim3(kWave * WPR),
+                     0, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                     static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout), a.rows, a.sx,
+                     a.sr, a.sy, a.srout, 1.0f / static_cast<float>(a.hidden), a.eps, xcd_runs);
+  return hipGetLastError();
+}
+
+template <typename T, typename W, bool RES>
+hipError_t run_pipe_shape(const RegShape& s, const RmsArgs& a, hipStream_t stream) {
+#define AKO_PIPE_SHAPE(WPR, VPT) \
+  if (s.wpr == WPR && s.vpt == VPT) return run_pipe<T, W, WPR, VPT, RES>(a, stream);
+  AKO_PIPE_SHAPE(4, 2)
+  AKO_PIPE_SHAPE(8, 1)
+  AKO_PIPE_SHAPE(8, 2)
+  AKO_PIPE_SHAPE(16, 1)
+  AKO_PIPE_SHAPE(16, 2)
+  AKO_PIPE_SHAPE(16, 4)
+#undef AKO_PIPE_SHAPE
+  return hipErrorInvalidValue;
+}
+
 template <typename T, typename W, bool RES>
 hipError_t run_reg_shape(const RegShape& s, const RmsArgs& a, hipStream_t stream) {
 #define AKO_RMS_SHAPE(WPR, VPT) \
@@ -571,7 +777,33 @@ hipError_t run_typed(const RmsArgs& a, hipStream_t stream) {
   const bool reg = a.vector_ok && g_rms_tuning.force_stream == 0 && nvec <= kMaxRegPackets &&
                    nvec >= 1;
   if (!reg) return a.residual ? run_stream<T, W, true>(a, stream) : run_stream<T, W, false>(a, stream);
-  const RegShape s = pick_shape(nvec, a.residual, a.rows);
+  RegShape s = pick_shape(nvec, a.residual, a.rows);
+  // The pipelined kernel takes full rows only (no packet past the row's end)
+  // and launches of many rows. By default it runs rows of 512 or 1024
+  // packets whose inputs (x, and the residual) total at most 16 KiB, as one
+  // packet per lane per tensor over nvec / 64 wavefronts. Medians of five
+  // cold back-to-back runs on MI355X, 16384 rows, against rmsnorm_reg's
+  // default: plain rows of 4096 half elements 5947 -> 6568 GB/s, residual
+  // rows of 4096 6143 -> 6978, plain rows of 8192 6340 -> 7001, fp32 rows of
+  // 2048 and 4096 +10-15% alike. Rows of 32 KiB of input (residual 8192,
+  // plain and residual 16384), and two packets per lane at any width, were
+  // 3-18% slower pipelined. Plain rows need 16 rows per workgroup: with 2-4
+  // (512 or 2048 rows) they ran 7-15% slower than rmsnorm_reg, while
+  // residual rows were as fast or faster from 300 rows up.
+  const bool rows_ok = a.rows > kFewRows && a.rows < (int64_t(1) << 31) && nvec * E == a.hidden;
+  const bool forced_shape = g_rms_tuning.waves_per_row > 0 || g_rms_tuning.vecs_per_thread > 0;
+  bool pipe = false;
+  if (g_rms_tuning.pipeline == 2) {
+    pipe = rows_ok && int64_t(s.wpr) * kWave * s.vpt == nvec && pipe_shape(s);
+  } else if (g_rms_tuning.pipeline == 0 && !forced_shape && rows_ok && (nvec == 512 || nvec == 1024) &&
+             a.hidden * static_cast<int64_t>(sizeof(T)) * (a.residual ? 2 : 1) <= kPipeMaxRowBytes) {
+    const RegShape one{static_cast<int>(nvec / kWave), 1};
+    if (a.residual || a.rows >= kPipeMinRowsPerBlock * pipe_blocks(one.wpr, false, a.rows)) {
+      s = one;
+      pipe = true;
+    }
+  }
+  if (pipe) return a.residual ? run_pipe_shape<T, W, true>(s, a, stream) : run_pipe_shape<T, W, false>(s, a, stream);
   return a.residual ? run_reg_shape<T, W, true>(s, a, stream)
                     : run_reg_shape<T, W, false>(s, a, stream);
 }

@@ -219,6 +219,7 @@ def test_rmsnorm_split_launches_match_one_launch(cap: int) -> None:
 
     cases = [(301, 256), (259, 4096), (97, 140_000)]  # 4 rows per block, XCD-ordered wide rows, two-pass
     try:
+        _native.set_tuning(0, 9, 1)  # one row per workgroup (the persistent kernel never splits)
         for rows, hidden in cases:
             x = grandn((rows, hidden), torch.bfloat16, 33)
             r = grandn((rows, hidden), torch.bfloat16, 34)
@@ -234,6 +235,100 @@ def test_rmsnorm_split_launches_match_one_launch(cap: int) -> None:
         assert_oracle(ey, to_np(rmsnorm_hip(x, w)), torch.bfloat16)
     finally:
         _native.set_tuning(0, 7, 0)
+        _native.set_tuning(0, 9, 0)
+
+
+# (dtype, weight dtype, hidden, forced (waves per row, packets per lane) or None).
+# Every shape with a pipelined instantiation appears; None is the default shape
+# of a launch of many rows (full rows: hidden = 64 * waves * packets * E).
+PIPE_CASES = [
+    (torch.float16, torch.float16, 4096, None),      # plain (4, 2), residual (8, 1)
+    (torch.bfloat16, torch.bfloat16, 8192, None),    # plain (8, 2), residual (16, 1)
+    (torch.bfloat16, torch.float32, 16384, None),    # (16, 2), fp32 weight
+    (torch.float16, torch.float16, 32768, None),     # (16, 4)
+    (torch.float32, torch.float32, 2048, None),      # fp32 rows, (4, 2) / (8, 1)
+    (torch.float16, torch.float32, 8192, (8, 1)),
+    (torch.bfloat16, torch.bfloat16, 16384, (16, 1)),
+    (torch.float32, torch.float32, 4096, (16, 1)),
+]
+
+
+@pytest.mark.parametrize("dtype,w_dtype,hidden,shape", PIPE_CASES,
+                         ids=[f"{NAMES[d]}-{NAMES[w]}-{h}-{s}" for d, w, h, s in PIPE_CASES])
+def test_rmsnorm_pipelined_kernel_matches_register_kernel(dtype, w_dtype, hidden, shape) -> None:
+    """The persistent, software-pipelined kernel (key 9 = 2) against the
+    one-row-per-workgroup kernel (key 9 = 1): the same arithmetic in the same
+    order, so outputs must be bit-identical, for both row orders (key 5),
+    several grid sizes (key 10: 1 and 3 workgroups per CU, 32 leaves most
+    workgroups one row or none) and row counts with odd and even trips per
+    workgroup, empty XCD ranges and a strided input. One case per dtype is
+    also checked against the oracle."""
+    from ako_amd import _native
+
+    rows_list = [257, 1031, 4099] + ([16384] if hidden <= 8192 else []) if hidden <= 16384 else [257, 1031]
+    try:
+        if shape is not None:
+            _native.set_tuning(0, 1, shape[0])
+            _native.set_tuning(0, 2, shape[1])
+        for rows in rows_list:
+            base = grandn((rows, hidden + 64), dtype, 40 + rows)
+            x = base[:, :hidden]  # row stride hidden + 64
+            r = grandn((rows, hidden), dtype, 41 + rows)
+            w = grandn((hidden,), w_dtype, 42, scale=0.1, shift=1.0)
+            for key in (5, 10):  # left set by the previous row count's sweep
+                _native.set_tuning(0, key, 0)
+            _native.set_tuning(0, 9, 1)
+            want_p = rmsnorm_hip(x, w)
+            want_y, want_s = rmsnorm_residual_hip(x, r, w)
+            if rows == rows_list[0]:
+                assert_oracle(oracle.rmsnorm(to_np(x), to_np(w), dtype=NAMES[dtype], w_dtype=NAMES[w_dtype]),
+                              to_np(want_p), dtype)
+            # The default choice. Rows of 512 or 1024 packets go pipelined at
+            # one packet per lane (when their input fits 16 KiB; plain rows
+            # only with 16 rows per workgroup, as at 16384 rows) or to the
+            # register kernel's one-packet residual shape: either way the
+            # register kernel at (packets / 64, 1) sums in the same order.
+            # Plain rows short of the row count take the register kernel's
+            # own default shape.
+            nvec = hidden * x.element_size() // 16
+            if shape is None and nvec in (512, 1024):
+                _native.set_tuning(0, 1, nvec // 64)
+                _native.set_tuning(0, 2, 1)
+                want_dp = rmsnorm_hip(x, w)
+                want_dy, _ = rmsnorm_residual_hip(x, r, w)
+                _native.set_tuning(0, 1, 0)
+                _native.set_tuning(0, 2, 0)
+            else:
+                want_dp, want_dy = want_p, want_y
+            _native.set_tuning(0, 9, 0)
+            got_p = rmsnorm_hip(x, w)
+            got_y, got_s = rmsnorm_residual_hip(x, r, w)
+            assert torch.equal(got_y, want_dy), rows
+            if shape is None and nvec in (512, 1024) and rows >= 16384:
+                assert torch.equal(got_p, want_dp), rows
+            else:
+                assert torch.equal(got_p, want_dp) or torch.equal(got_p, want_p), rows
+            assert torch.equal(got_s, want_s), rows
+            if rows == rows_list[0]:
+                ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype=NAMES[dtype],
+                                                 w_dtype=NAMES[w_dtype])
+                assert_oracle(ey, to_np(got_y), dtype)
+                np.testing.assert_array_equal(to_np(got_s), es)
+                assert_oracle(oracle.rmsnorm(to_np(x), to_np(w), dtype=NAMES[dtype], w_dtype=NAMES[w_dtype]),
+                              to_np(got_p), dtype)
+            _native.set_tuning(0, 9, 2)
+            for order in (0, 1):
+                _native.set_tuning(0, 5, order)
+                for per_cu in (0, 1, 3, 32):
+                    _native.set_tuning(0, 10, per_cu)
+                    tag = (rows, order, per_cu)
+                    assert torch.equal(rmsnorm_hip(x, w), want_p), tag
+                    y, s = rmsnorm_residual_hip(x, r, w)
+                    assert torch.equal(s, want_s), tag
+                    assert torch.equal(y, want_y), tag
+    finally:
+        for key in (1, 2, 5, 9, 10):
+            _native.set_tuning(0, key, 0)
 
 
 def test_rmsnorm_empty_and_errors() -> None:
