@@ -2,10 +2,12 @@
 // device copy (16-byte packets, one per lane, non-temporal loads and stores)
 // at given byte counts, with cold buffers.
 //
-// A streaming kernel that reads and writes B bytes cannot be expected to beat
-// a copy that moves the same B bytes, so the copy's fraction of the HBM peak at
-// that size is the practical roofline of each hot-path cell. It falls with
-// size because every launch pays a roughly fixed ramp-up and drain.
+// The copy's fraction of the HBM peak at a cell's byte count is the reference
+// each hot-path cell is compared with: what the plainest stream of the same
+// bytes reaches on the same box. It is not a strict bound (a kernel that
+// orders its reads and writes differently can pass it, as the pipelined
+// RMSNorm does by a few percent). It falls with size because every launch
+// pays a roughly fixed ramp-up and drain.
 //
 // Usage: copy_ceiling [bytes_per_buffer ...]   (default: the hot-path cell sizes)
 // Prints one JSON object per size, block shape and store policy:

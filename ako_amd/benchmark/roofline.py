@@ -235,9 +235,10 @@ def copy_same_bytes(alg_bytes: int, *, timeout_s: float = 120.0) -> dict[str, An
     """Time a plain device copy that moves about ``alg_bytes`` (half read, half
     written) with ``ako_amd/_lib/copy_ceiling``, run as a child process.
 
-    It is the practical ceiling for a streaming kernel of that size: launches
-    pay a roughly fixed ramp-up, so the copy's share of the HBM peak falls with
-    the byte count. Returns the probe's record for its fastest block shape, or
+    It is the reference for a streaming kernel of that size (what the plainest
+    stream of those bytes reaches; a kernel that orders its traffic otherwise
+    can pass it): launches pay a roughly fixed ramp-up, so the copy's share of
+    the HBM peak falls with the byte count. Returns the probe's record for its fastest block shape, or
     None when the probe is not built or fails (it is a reference figure, not
     part of any result)."""
     import subprocess

@@ -14,7 +14,8 @@ Also reported on the same line:
   roofline      the dominant kernel (the slowest launch of the step) with its
                 per-launch duration from HIP events on the launch stream, and
                 a plain device copy of the same byte count timed the same way
-                (copy_same_bytes: the size's practical ceiling);
+                (copy_same_bytes: what the plainest stream of those bytes
+                reaches; a reference, which a kernel can pass);
   per_kernel    every launch of the step, each beside its copy ceiling, by
                 per-launch events (as the roofline) and, under back_to_back,
                 on its own as 60 launches between one event pair over cold
@@ -311,7 +312,7 @@ def rope_prefill_summary(extras, ceilings):
                     "copy_pct_hbm_peak": qk.get("copy_pct_hbm_peak"), "kernel_over_copy": qk.get("kernel_over_copy")}
         if k is not None:
             out[tag]["k_alone"] = {"pct_hbm_peak": k["pct_hbm_peak"], "copy_pct_hbm_peak": k.get("copy_pct_hbm_peak"),
-                                   "note": "34 MB launch: bounded by the copy ceiling of that size"}
+                                   "note": "34 MB launch: a copy of that size reaches little more"}
     return out
 
 
