@@ -66,6 +66,49 @@ def test_rmsnorm_random_cases(seed: int) -> None:
         _check(ey, y, dtype, case)
 
 
+@pytest.mark.parametrize("seed", seeds(4))
+def test_rmsnorm_pipelined_random_cases(seed: int) -> None:
+    """Launches of many full rows (the persistent pipelined kernel's domain),
+    with random row counts, padded strides, weight dtypes and pipelined grid
+    settings (key 9: default or forced; key 10: workgroups per CU; key 5: row
+    order), against the oracle on a seeded sample of rows (rows are computed
+    independently, so sampled rows check the launch)."""
+    from ako_amd import _native
+
+    rng = np.random.default_rng(5000 + seed)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    widths = {torch.float32: [2048, 4096], torch.float16: [4096, 8192], torch.bfloat16: [4096, 8192]}
+    try:
+        for _ in range(4):
+            dtype = DTYPES[rng.integers(3)]
+            rows = int(rng.choice([257, 1000, 4099, 9001, 16500]))
+            hidden = int(rng.choice(widths[dtype]))
+            pad = int(rng.choice([0, 8, 64]))
+            w_fp32 = dtype != torch.float32 and rng.random() < 0.3
+            pipeline, per_cu, order = int(rng.choice([0, 2])), int(rng.choice([0, 1, 2, 3, 5])), int(rng.choice([0, 1]))
+            _native.set_tuning(0, 9, pipeline)
+            _native.set_tuning(0, 10, per_cu)
+            _native.set_tuning(0, 5, order)
+            x = _padded(rows, hidden, pad, dtype, gen)
+            r = _padded(rows, hidden, pad, dtype, gen)
+            w = (torch.randn(hidden, generator=gen, device=DEV) * 0.1 + 1.0).to(torch.float32 if w_fp32 else dtype)
+            pick = np.unique(np.concatenate([[0, rows - 1], rng.choice(rows, size=62, replace=False)]))
+            idx = torch.as_tensor(pick, device=DEV)
+            case = (f"rows={rows} hidden={hidden} pad={pad} {dtype} w_fp32={w_fp32} "
+                    f"pipeline={pipeline} per_cu={per_cu} order={order}")
+            wname = "float32" if w_fp32 else NAMES[dtype]
+            xs, rs, wn = to_np(x[idx]), to_np(r[idx]), to_np(w)
+            _check(oracle.rmsnorm(xs, wn, 1e-6, dtype=NAMES[dtype], w_dtype=wname),
+                   rmsnorm_hip(x, w, 1e-6)[idx], dtype, case)
+            y, s = rmsnorm_residual_hip(x, r, w, 1e-6)
+            ey, es = oracle.rmsnorm_residual(xs, rs, wn, 1e-6, dtype=NAMES[dtype], w_dtype=wname)
+            np.testing.assert_array_equal(to_np(s[idx]), es, err_msg=case)
+            _check(ey, y[idx], dtype, case)
+    finally:
+        for key in (5, 9, 10):
+            _native.set_tuning(0, key, 0)
+
+
 @pytest.mark.parametrize("seed", seeds(6))
 def test_rope_random_cases(seed: int) -> None:
     rng = np.random.default_rng(2000 + seed)
