@@ -707,11 +707,14 @@ def test_rope_every_finite_half_value(dtype, style) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_rmsnorm_extreme_rows(dtype) -> None:
+@pytest.mark.parametrize("copies", [1, 1821], ids=["9rows", "16389rows"])
+def test_rmsnorm_extreme_rows(dtype, copies) -> None:
     """Rows of subnormals, rows near the format's maximum (whose sum of squares
     overflows fp32 for bf16), a single non-zero element, zeros, and mixes,
     plain and residual: element by element within 1 ulp of the oracle (the
-    rounded residual sum exactly)."""
+    rounded residual sum exactly). The nine rows run as one launch of nine
+    (the register kernel) and repeated 1821 times, which the persistent
+    pipelined kernel takes."""
     rng = np.random.default_rng(37)
     h = 4096
     if dtype == torch.float16:
@@ -731,12 +734,18 @@ def test_rmsnorm_extreme_rows(dtype) -> None:
     x = _bits_tensor(np.stack(rows), dtype)
     r = _bits_tensor(np.stack(rows[::-1]), dtype)
     w = grandn((h,), dtype, 41, scale=0.1, shift=1.0)
+    big_x, big_r = x.repeat(copies, 1), r.repeat(copies, 1)
+
+    def tiled(a: np.ndarray) -> np.ndarray:
+        return np.tile(a, (copies, 1))
+
     for eps in (1e-6, 0.0):
-        y = rmsnorm_hip(x, w, eps)
-        dist = _ulp_dist(y, oracle.rmsnorm(to_np(x), to_np(w), eps, dtype=NAMES[dtype]))
+        y = rmsnorm_hip(big_x, w, eps)
+        dist = _ulp_dist(y, tiled(oracle.rmsnorm(to_np(x), to_np(w), eps, dtype=NAMES[dtype])))
         assert dist.max() <= 1, f"plain eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
-        y, s = rmsnorm_residual_hip(x, r, w, eps)
+        y, s = rmsnorm_residual_hip(big_x, big_r, w, eps)
         ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), eps, dtype=NAMES[dtype])
+        ey, es = tiled(ey), tiled(es)
         assert _ulp_dist(s, es).max() == 0
         dist = _ulp_dist(y, ey)
         assert dist.max() <= 1, f"residual eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
