@@ -284,6 +284,21 @@ class Attention(nn.Module):
             self.v_proj = nn.Linear(config.hidden_dim, kv_dim, bias=False)
         self.o_proj = nn.Linear(config.hidden_dim, config.hidden_dim, bias=False)
 
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        """State dicts of either layout load into either: three ``q/k/v_proj``
+        matrices (the reference's layout, ``ako/models/decoder.py:153-156``)
+        are stacked into ``qkv_proj``, and a ``qkv_proj`` is split back."""
+        names = [prefix + f"{n}_proj.weight" for n in ("q", "k", "v")]
+        fused = prefix + "qkv_proj.weight"
+        if self.config.fused_qkv and all(n in state_dict for n in names):
+            state_dict[fused] = torch.cat([state_dict.pop(n) for n in names], 0)
+        elif not self.config.fused_qkv and fused in state_dict:
+            h = self.config.hidden_dim
+            q, k, v = state_dict.pop(fused).split([h, self.kv_dim, self.kv_dim], 0)
+            for n, t in zip(names, (q, k, v)):
+                state_dict[n] = t
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+
     @torch.no_grad()
     def load_qkv(self, q_weight: torch.Tensor, k_weight: torch.Tensor, v_weight: torch.Tensor) -> None:
         """Set the q, k and v projections from three ``(out, hidden)`` matrices

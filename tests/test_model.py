@@ -169,3 +169,22 @@ def test_stack_matches_hugging_face_llama(n_kv_heads: int, fused_qkv: bool) -> N
                 for t in range(9, 12):
                     got.append(stack(emb[:, t:t + 1], kv_cache=cache)[:, -1])
                 assert_close(torch.stack(got, 1), want[:, 8:12], atol=1e-5, rtol=1e-5)
+
+
+def test_state_dicts_load_across_projection_layouts() -> None:
+    """A state dict with three q/k/v matrices (the reference's layout) loads
+    into the fused model and the other way round; outputs are unchanged."""
+    import dataclasses
+
+    separate = build_stack(dataclasses.replace(SMALL, fused_qkv=False), backend="torch", seed=5).eval()
+    fused = build_stack(dataclasses.replace(SMALL, fused_qkv=True), backend="torch", seed=9).eval()
+    fused.load_state_dict(separate.state_dict())
+    x = torch.randn(2, 7, SMALL.hidden_dim)
+    with torch.no_grad():
+        want = separate(x)
+        assert_close(fused(x), want, atol=1e-6, rtol=1e-6)
+        back = build_stack(dataclasses.replace(SMALL, fused_qkv=False), backend="torch", seed=11).eval()
+        back.load_state_dict(fused.state_dict())
+        assert_close(back(x), want, atol=1e-6, rtol=1e-6)
+    assert "layers.0.attention.qkv_proj.weight" in fused.state_dict()
+    assert "layers.0.attention.q_proj.weight" in back.state_dict()
