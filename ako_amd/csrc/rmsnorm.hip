@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "launch.h"
@@ -80,7 +81,8 @@ __device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, unsigned
   return full * 8 * chunk + x * rest + (i - full * chunk);
 }
 
-template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS, bool EW>
+template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS, bool EW,
+          bool SPLIT = false>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     T* __restrict__ y, T* __restrict__ rout, int64_t row0, int64_t rows, int hidden, int64_t sx,
@@ -90,8 +92,10 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   // Packets are processed in groups: every load of a group is issued before
   // the first of them is consumed, so a lane's memory latency is paid once
   // per group rather than once per packet. Groups stay small enough that x,
-  // the residual and the prefetched weights fit in registers.
-  constexpr int G = VPT <= 4 ? VPT : (VPT <= 8 ? 4 : 2);
+  // the residual and the prefetched weights fit in registers. SPLIT makes
+  // every packet its own group (the next packet's loads are issued after the
+  // previous one is added, stored and squared).
+  constexpr int G = SPLIT ? 1 : (VPT <= 4 ? VPT : (VPT <= 8 ? 4 : 2));
   static_assert(VPT % G == 0, "VPT must be a multiple of the group size");
   // With few packets per lane the first weight group is fetched before the
   // reduction; with many, registers are kept for x and weights come per group.
@@ -589,7 +593,7 @@ int64_t max_blocks_per_launch(int threads_per_block) {
   return forced > 0 ? std::min(cap, forced) : cap;
 }
 
-template <typename T, typename W, int WPR, int VPT, bool RES, bool EW>
+template <typename T, typename W, int WPR, int VPT, bool RES, bool EW, bool SPLIT = false>
 hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   constexpr int RPB = WPR >= 4 ? 1 : 4 / WPR;
   const dim3 block(kWave * WPR * RPB);
@@ -615,8 +619,8 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
     if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
     if (g_rms_tuning.row_order == 2)
       xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
-    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0, EW>), grid,
-                       block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0, EW, SPLIT>),
+                       grid, block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                        static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                        b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
                        1.0f / static_cast<float>(a.hidden), a.eps, xcd_chunk);
@@ -646,6 +650,17 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
                     (forced == 0 && a.rows <= kFewRows &&
                      a.hidden * static_cast<int64_t>(sizeof(T)) <= kEarlyWeightRowBytes);
     if (ew) return run_reg_launch<T, W, WPR, VPT, RES, true>(a, stream);
+  }
+  // One packet per load group for bf16 residual rows of 16 wavefronts x 2
+  // packets (rows of 8193-16384 elements), launches of many rows.
+  // Interleaved medians of 10 rounds on MI355X, 16384 x 16384, cold inputs:
+  // bf16 +1.5% back to back and +1.9% per launch (two separate runs: +1.5 to
+  // +1.9%); fp16 -0.3%, so fp16 keeps whole groups, as do plain rows (-1.4%
+  // bf16, -3.5% fp16).
+  if constexpr (VPT == 2 && WPR == 16 && RES) {
+    const int forced = g_rms_tuning.load_groups;
+    const bool split = forced == 2 || (forced == 0 && std::is_same_v<T, __bf16> && a.rows > kFewRows);
+    if (split) return run_reg_launch<T, W, WPR, VPT, RES, false, true>(a, stream);
   }
   return run_reg_launch<T, W, WPR, VPT, RES, false>(a, stream);
 }

@@ -238,6 +238,34 @@ def test_rmsnorm_split_launches_match_one_launch(cap: int) -> None:
         _native.set_tuning(0, 9, 0)
 
 
+@pytest.mark.parametrize("dtype,w_dtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                           (torch.float16, torch.float16)])
+def test_rmsnorm_residual_load_groups_match(dtype, w_dtype) -> None:
+    """The residual (16 wavefronts, 2 packets) rows with both packets loaded
+    as one group (key 11 = 1) and one packet at a time (key 11 = 2): the same
+    sums in the same order, so bit-identical outputs, at a decode-sized and a
+    many-row launch; the default choice against the oracle."""
+    from ako_amd import _native
+
+    h = 16384
+    try:
+        for rows in (33, 300):
+            x = grandn((rows, h), dtype, 60 + rows)
+            r = grandn((rows, h), dtype, 61 + rows)
+            w = grandn((h,), w_dtype, 62, scale=0.1, shift=1.0)
+            outs = {}
+            for key in (1, 2, 0):
+                _native.set_tuning(0, 11, key)
+                outs[key] = rmsnorm_residual_hip(x, r, w)
+            assert all(torch.equal(a, b) for a, b in zip(outs[1], outs[2])), rows
+            assert all(torch.equal(a, b) for a, b in zip(outs[0], outs[1])), rows
+            ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype=NAMES[dtype], w_dtype=NAMES[w_dtype])
+            np.testing.assert_array_equal(to_np(outs[0][1]), es)
+            assert_oracle(ey, to_np(outs[0][0]), dtype)
+    finally:
+        _native.set_tuning(0, 11, 0)
+
+
 # (dtype, weight dtype, hidden, forced (waves per row, packets per lane) or None).
 # Every shape with a pipelined instantiation appears; None is the default shape
 # of a launch of many rows (full rows: hidden = 64 * waves * packets * E).
