@@ -81,6 +81,11 @@ def test_hip_graph_replays_match_eager() -> None:
     k = _rand(1, 1, 8, 128, seed=4)
     cos, sin = build_rope_tables(1, 128, device=DEV)
     g, u = _rand(1, 14336, seed=5), _rand(1, 14336, seed=6)
+    # Launches of many rows: the persistent pipelined kernel (4096-wide rows)
+    # and bf16 residual rows of 16384 with one-packet load groups.
+    xp, rp = _rand(9000, 4096, seed=7), _rand(9000, 4096, seed=8)
+    xb, rb = _rand(300, 16384, seed=9), _rand(300, 16384, seed=10)
+    wb = _rand(16384, seed=11, scale=0.1, shift=1.0)
 
     def step():
         a = rmsnorm_hip(x, w)
@@ -88,7 +93,10 @@ def test_hip_graph_replays_match_eager() -> None:
         d = rope_hip(q, cos, sin)
         e, f = rope_qk_hip(q, k, cos, sin, "interleaved")
         h = swiglu_hip(g, u)
-        return a, b, c, d, e, f, h
+        i = rmsnorm_hip(xp, w)
+        j, m = rmsnorm_residual_hip(xp, rp, w)
+        n, o = rmsnorm_residual_hip(xb, rb, wb)
+        return a, b, c, d, e, f, h, i, j, m, n, o
 
     eager = step()
     side = torch.cuda.Stream()
