@@ -653,7 +653,7 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   }
   // One packet per load group for bf16 residual rows of 16 wavefronts x 2
   // packets (rows of 8193-16384 elements), launches of many rows.
-  // Interleaved medians of 10 rounds on MI355X, 16384 x 16384, cold inputs:
+  // Medians of 10 interleaved repetitions on MI355X, 16384 x 16384, cold inputs:
   // bf16 +1.5% back to back and +1.9% per launch (two separate runs: +1.5 to
   // +1.9%); fp16 -0.3%, so fp16 keeps whole groups, as do plain rows (-1.4%
   // bf16, -3.5% fp16).
