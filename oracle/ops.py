@@ -98,7 +98,7 @@ def rmsnorm_residual(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float = 1
     in the storage dtype (fp32 add, rounded), then normalised."""
     if np.shape(x) != np.shape(r):
         raise ValueError(f"Shape mismatch: x {np.shape(x)} vs residual {np.shape(r)}")
-    with np.errstate(over="ignore"):
+    with np.errstate(over="ignore", invalid="ignore"):  # inf + -inf is NaN, as on the GPU
         s = round_to(to_f32(x, dtype) + to_f32(r, dtype), dtype)
     return rmsnorm(s, w, eps, dtype=dtype, w_dtype=w_dtype), s
 

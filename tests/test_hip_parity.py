@@ -779,6 +779,61 @@ def test_rmsnorm_extreme_rows(dtype, copies) -> None:
         assert dist.max() <= 1, f"residual eps={eps}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
 
 
+def _with_specials(shape, dtype, seed: int, hits: list[tuple[tuple, float]]) -> torch.Tensor:
+    """Seeded N(0,1) values with the given (index, value) entries overwritten."""
+    t = grandn(shape, torch.float32, seed)
+    for idx, val in hits:
+        t[idx] = val
+    return t.to(dtype)
+
+
+@pytest.mark.parametrize("copies", [1, 1100], ids=["16rows", "17600rows"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_nonfinite_inputs_propagate_like_the_oracle(dtype, copies) -> None:
+    """NaN and infinities in the inputs: every kernel gives the oracle's
+    results, NaN where the oracle has NaN (any payload) and the same numbers
+    elsewhere (RMSNorm and SwiGLU within 1 ulp, RoPE exactly). A row holding
+    an infinity has an infinite sum of squares, so its finite elements
+    normalise to 0 and the infinity to NaN (inf * 0), as in the unfused
+    reference. RMSNorm runs both as 16 rows (the register kernel) and
+    repeated 1100 times (17600 rows: the pipelined kernel; bf16 residual rows
+    of this width keep the register kernel)."""
+    inf, nan = float("inf"), float("nan")
+    h = 4096
+    x = _with_specials((16, h), dtype, 70, [((0, 5), inf), ((1, 9), -inf), ((2, 100), nan), ((3, 1), inf),
+                                             ((3, 2), -inf), ((7, 300), inf), ((9, 0), nan), ((9, 1), inf)])
+    r = _with_specials((16, h), dtype, 71, [((5, 17), inf), ((6, 33), nan), ((7, 300), -inf), ((8, 4), -inf)])
+    w = grandn((h,), dtype, 72, scale=0.1, shift=1.0)
+    bx, br = x.repeat(copies, 1), r.repeat(copies, 1)
+
+    def tiled(a):
+        return np.tile(a, (copies, 1))
+
+    dist = _ulp_dist(rmsnorm_hip(bx, w), tiled(oracle.rmsnorm(to_np(x), to_np(w), dtype=NAMES[dtype])))
+    assert dist.max() <= 1, f"rmsnorm: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+    y, s_ = rmsnorm_residual_hip(bx, br, w)
+    ey, es = oracle.rmsnorm_residual(to_np(x), to_np(r), to_np(w), dtype=NAMES[dtype])
+    assert _ulp_dist(s_, tiled(es)).max() == 0
+    dist = _ulp_dist(y, tiled(ey))
+    assert dist.max() <= 1, f"rmsnorm_residual: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+    if copies > 1:
+        return
+    q = _with_specials((2, 8, 4, 128), dtype, 73, [((0, 1, 0, 3), inf), ((0, 2, 1, 70), -inf), ((1, 3, 2, 0), nan),
+                                                   ((1, 7, 3, 64), inf), ((1, 7, 3, 0), nan)])
+    cos, sin = build_rope_tables(8, 128, device=DEV)
+    cos, sin = cos.to(dtype), sin.to(dtype)
+    for style in ("neox", "interleaved"):
+        dist = _ulp_dist(rope_hip(q, cos, sin, style),
+                         oracle.rope(to_np(q), to_np(cos), to_np(sin), style, dtype=NAMES[dtype],
+                                     table_dtype=NAMES[dtype]))
+        assert dist.max() == 0, f"rope {style}: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+    g = _with_specials((64, h), dtype, 74, [((0, 0), inf), ((1, 1), -inf), ((2, 2), nan), ((3, 3), 0.0),
+                                             ((4, 4), 1.0)])
+    u = _with_specials((64, h), dtype, 75, [((3, 3), inf), ((4, 4), -inf), ((5, 5), nan), ((6, 6), inf)])
+    dist = _ulp_dist(swiglu_hip(g, u), oracle.swiglu(to_np(g), to_np(u), dtype=NAMES[dtype]))
+    assert dist.max() <= 1, f"swiglu: {dist.max()} ulp; {int((dist > 0).sum())} differ"
+
+
 def _ordered32(a: np.ndarray) -> np.ndarray:
     b = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.int64)
     return np.where(b & 0x80000000, 0x80000000 - (b & 0x7FFFFFFF), 0x80000000 + b)
