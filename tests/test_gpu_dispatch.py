@@ -287,3 +287,41 @@ def test_config5_workload_selection(tmp_path) -> None:
     for op in ops.values():
         assert op["source"] == "benchmark" and all(r["passed"] for r in op["ulp_reports"] if r["kernel"].endswith("_hip"))
     assert len(hip) >= 9, hip
+
+
+def test_minimal_reference_side_binding() -> None:
+    """The least a maintainer of the reference would write to bind the C ABI
+    (a fresh ctypes handle, the declared argument types, raw pointers and the
+    current stream): the same bits as this package's wrapper, and the status
+    and message contract on a bad argument."""
+    import ctypes
+
+    from ako_amd._native import library_path
+
+    lib = ctypes.CDLL(str(library_path()))
+    lib.ako_rmsnorm_fwd.restype = ctypes.c_int
+    lib.ako_rmsnorm_fwd.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4 + \
+        [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.ako_last_error.restype = ctypes.c_char_p
+    codes = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+    def rmsnorm_minimal(x, weight, eps=1e-6):
+        h = x.shape[-1]
+        x2 = x.contiguous()
+        y = torch.empty_like(x2)
+        rc = lib.ako_rmsnorm_fwd(x2.data_ptr(), weight.contiguous().data_ptr(), y.data_ptr(),
+                                 x2.numel() // h, h, h, h, eps, codes[x.dtype], codes[weight.dtype],
+                                 torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise (ValueError if rc in (1, 2) else RuntimeError)(lib.ako_last_error().decode())
+        return y.view(x.shape)
+
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        x = _rand(3, 700, 4096, dtype=dtype, seed=80)
+        w = _rand(4096, dtype=dtype, seed=81, scale=0.1, shift=1.0)
+        assert torch.equal(rmsnorm_minimal(x, w), rmsnorm_hip(x, w, 1e-6))
+        w32 = w.float()
+        assert torch.equal(rmsnorm_minimal(x, w32), rmsnorm_hip(x, w32, 1e-6))
+    with pytest.raises(ValueError, match="eps"):
+        rmsnorm_minimal(x, w, -1.0)
+
