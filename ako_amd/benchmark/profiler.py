@@ -50,6 +50,11 @@ def _device_us(event: Any) -> float:
     return 0.0
 
 
+def _is_host_event(event: Any) -> bool:
+    kind = getattr(event, "device_type", None)
+    return kind is not None and str(kind).rsplit(".", 1)[-1] == "CPU"
+
+
 def kernel_table(prof: torch.profiler.profile, *, device: bool | None = None) -> list[dict[str, Any]]:
     """Rows ``{name, calls, total_us, avg_us, share}`` sorted by total time.
 
@@ -62,6 +67,10 @@ def kernel_table(prof: torch.profiler.profile, *, device: bool | None = None) ->
         device = any(_device_us(e) > 0 for e in events)
     rows = []
     for e in events:
+        # Device rows are kernels only: a host op (aten::mm) also reports the
+        # device time of the kernels it launched, which would count them twice.
+        if device and _is_host_event(e):
+            continue
         total = _device_us(e) if device else float(getattr(e, "self_cpu_time_total", 0.0) or 0.0)
         if total <= 0:
             continue

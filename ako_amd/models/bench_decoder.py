@@ -35,6 +35,38 @@ def _timed(fn) -> tuple[Any, float]:
     return out, (time.perf_counter() - t0) * 1e3
 
 
+def _fold(rows: list[dict[str, Any]], share: dict[str, Any], per: int) -> dict[str, Any]:
+    return {
+        "device_us": round(share["total_us"] / per, 1),
+        "library_us": round(share["library_us"] / per, 1),
+        "library_share": round(share["share"], 4),
+        "library_launches": round(share["library_calls"] / per, 2),
+        "library_kernels": share["library_kernels"],
+        "top": [{"name": r["name"][:80], "us": round(r["total_us"] / per, 2),
+                 "calls": round(r["calls"] / per, 2)} for r in rows[:8]],
+    }
+
+
+def prefill_breakdown(model, prompt: torch.Tensor, passes: int = 5) -> dict[str, Any]:
+    """Where a prefill pass's device time goes (``passes`` prefills into fresh
+    caches under ``torch.profiler``, folded by kernel name, per pass), with
+    the share of this library's kernels."""
+    from ako_amd.benchmark.profiler import kernel_table, library_share, profile_cuda
+
+    caches = [model.stack.new_kv_cache(prompt.shape[1] + 1) for _ in range(passes)]
+    model.logits_last(prompt, model.stack.new_kv_cache(prompt.shape[1] + 1))  # warm
+    torch.cuda.synchronize()
+    with profile_cuda() as prof:
+        for cache in caches:
+            model.logits_last(prompt, cache)
+        torch.cuda.synchronize()
+    rows = kernel_table(prof, device=True)
+    share = library_share(rows)
+    if not rows or share["total_us"] <= 0:
+        return {"passes": passes, "recorded": False}
+    return {"passes": passes, "recorded": True, **_fold(rows, share, passes)}
+
+
 def graphed_step_breakdown(model, prompt: torch.Tensor, steps: int = 32) -> dict[str, Any]:
     """Where a graph-replayed decode step's device time goes: ``steps`` replays
     recorded with ``torch.profiler`` and folded by kernel name, with the share
@@ -108,6 +140,7 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
                 graphed_ms.append(t_g)
                 del runner
         step_breakdown = graphed_step_breakdown(model, prompt) if (graphed and breakdown) else None
+        prefill_parts = prefill_breakdown(model, prompt) if breakdown else None
     prefill = sorted(prefill_ms)[len(prefill_ms) // 2]
     dec = sorted(decode_ms)[len(decode_ms) // 2]
     extra = {}
@@ -129,6 +162,7 @@ def run_config5(backend: str, *, prompt_len: int = 512, decode_steps: int = 128,
         "tokens": tokens[0].tolist(),
         **extra,
         **({"graphed_step_breakdown": step_breakdown} if step_breakdown is not None else {}),
+        **({"prefill_breakdown": prefill_parts} if prefill_parts is not None else {}),
     }
 
 

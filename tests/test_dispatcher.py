@@ -289,6 +289,25 @@ def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
     assert abs(sum(r["share"] for r in rows) - 1.0) < 1e-9
 
 
+def test_kernel_table_counts_device_kernels_once() -> None:
+    """A host op that launched kernels also reports their device time; the
+    device table keeps the kernels only, so nothing counts twice."""
+    from types import SimpleNamespace
+
+    from torch.autograd import DeviceType
+
+    from ako_amd.benchmark.profiler import kernel_table
+
+    events = [SimpleNamespace(key="aten::mm", count=2, self_device_time_total=50.0, device_type=DeviceType.CPU),
+              SimpleNamespace(key="Cijk_gemm", count=2, self_device_time_total=50.0, device_type=DeviceType.CUDA),
+              SimpleNamespace(key="_ZN3ako11rmsnorm_reg", count=1, self_device_time_total=10.0,
+                              device_type=DeviceType.CUDA)]
+    prof = SimpleNamespace(key_averages=lambda: events)
+    rows = kernel_table(prof, device=True)
+    assert [r["name"] for r in rows] == ["Cijk_gemm", "_ZN3ako11rmsnorm_reg"]
+    assert sum(r["total_us"] for r in rows) == 60.0
+
+
 def test_library_share_counts_ako_kernels() -> None:
     from ako_amd.benchmark.profiler import library_share, table_markdown
 
