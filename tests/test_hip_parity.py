@@ -238,6 +238,37 @@ def test_rmsnorm_split_launches_match_one_launch(cap: int) -> None:
         _native.set_tuning(0, 9, 0)
 
 
+@pytest.mark.parametrize("hidden,rows", [(4096, 9000), (8192, 4100), (16384, 300)])
+def test_rmsnorm_padded_output_strides_through_the_abi(hidden, rows) -> None:
+    """Outputs with padded row strides, through the C ABI, at launch sizes the
+    pipelined kernel (4096 and 8192) and the one-packet load groups (bf16
+    16384) take: the padding is never written and the rows equal the
+    contiguous result."""
+    from ako_amd import _native
+
+    lib = _native.load()
+    dtype, pad = torch.bfloat16, 64
+    x = grandn((rows, hidden), dtype, 90)
+    r = grandn((rows, hidden), dtype, 91)
+    w = grandn((hidden,), dtype, 92, scale=0.1, shift=1.0)
+    want_y, want_s = rmsnorm_residual_hip(x, r, w)
+    want_p = rmsnorm_hip(x, w)
+    sentinel = -7.0
+    y = torch.full((rows, hidden + pad), sentinel, dtype=dtype, device=DEV)
+    s_ = torch.full((rows, hidden + pad), sentinel, dtype=dtype, device=DEV)
+    p = torch.full((rows, hidden + pad), sentinel, dtype=dtype, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    code = _native.DTYPE_CODES[dtype]
+    assert lib.ako_rmsnorm_residual_fwd(x.data_ptr(), r.data_ptr(), w.data_ptr(), y.data_ptr(), s_.data_ptr(),
+                                        rows, hidden, hidden, hidden, hidden + pad, hidden + pad, 1e-6, code, code,
+                                        stream) == 0
+    assert lib.ako_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), p.data_ptr(), rows, hidden, hidden, hidden + pad, 1e-6,
+                               code, code, stream) == 0
+    for out, want in ((y, want_y), (s_, want_s), (p, want_p)):
+        assert torch.equal(out[:, :hidden], want)
+        assert bool((out[:, hidden:] == sentinel).all())
+
+
 @pytest.mark.parametrize("dtype,w_dtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                            (torch.float16, torch.float16)])
 def test_rmsnorm_residual_load_groups_match(dtype, w_dtype) -> None:
