@@ -959,6 +959,22 @@ def test_tensors_beyond_2_31_elements() -> None:
     ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), 1e-6, dtype="float16")
     np.testing.assert_array_equal(to_np(s[sel]), es)
     assert _ulp_dist(y[sel], ey).max() <= 1
+    del r, y, s
+    # Plain rows of 8192 here take the persistent pipelined kernel.
+    y = rmsnorm_hip(x, w, 1e-6)
+    assert _ulp_dist(y[sel], oracle.rmsnorm(to_np(x[sel]), to_np(w), 1e-6, dtype="float16")).max() <= 1
+    del x, y
+    torch.cuda.empty_cache()
+
+    # bf16 residual rows of 16384: one-packet load groups.
+    rows = (1 << 31) // 16384 + 3
+    x, r = grandn((rows, 16384), torch.bfloat16, 82), grandn((rows, 16384), torch.bfloat16, 84)
+    w = grandn((16384,), torch.bfloat16, 86, scale=0.1, shift=1.0)
+    y, s = rmsnorm_residual_hip(x, r, w, 1e-6)
+    sel = pick(rows)
+    ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), 1e-6, dtype="bfloat16")
+    np.testing.assert_array_equal(to_np(s[sel]), es)
+    assert _ulp_dist(y[sel], ey).max() <= 1
     del x, r, y, s
     torch.cuda.empty_cache()
 
