@@ -17,7 +17,9 @@ parts apart: the ISA, the compute-unit count, the peak engine clock and the
 HBM size (``"AMD Radeon Graphics gfx950 256CU 2400MHz 288GB"``). An MI300X
 (gfx942, 304 CUs) and an MI355X (gfx950, 256 CUs, 2400 MHz) never share a key,
 nor do an MI350X and an MI355X (the same ISA and CU count, 2200 against
-2400 MHz).
+2400 MHz). Some boxes report an empty name instead of the generic one for the
+same part; ``part_label`` maps both to "AMD Radeon Graphics", so the key does
+not change from box to box.
 """
 
 from __future__ import annotations
@@ -96,11 +98,20 @@ def driver_label(module_version: str | None, hip_driver: int | None) -> str | No
     return None
 
 
+GENERIC_AMD_NAME = "AMD Radeon Graphics"
+_GENERIC_AMD_NAMES = {"", "amd radeon graphics", "amd gpu"}
+
+
 def part_label(name: str, arch: str | None, cus: int | None, clock_khz: int | None,
                mem_bytes: int | None) -> str:
     """HIP's device name followed by the fields that tell parts apart:
-    ``"<name> <isa> <cus>CU <MHz>MHz <GiB>GB"``; missing fields are left out."""
-    parts = [name.strip() or "AMD GPU"]
+    ``"<name> <isa> <cus>CU <MHz>MHz <GiB>GB"``; missing fields are left out.
+
+    Some boxes report the generic "AMD Radeon Graphics", others an empty name,
+    for the same part; both carry no information, so both become
+    ``GENERIC_AMD_NAME`` and one part keeps one cache key across boxes."""
+    base = name.strip()
+    parts = [GENERIC_AMD_NAME if base.lower() in _GENERIC_AMD_NAMES else base]
     if arch:
         parts.append(arch.split(":")[0])
     if cus:

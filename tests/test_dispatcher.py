@@ -202,17 +202,18 @@ _PARTS = {
 }
 
 
-def _fake_rocm_device(monkeypatch, part: str, *, library: bool = True):
+def _fake_rocm_device(monkeypatch, part: str, *, library: bool = True,
+                      name: str = "AMD Radeon Graphics"):
     from functools import lru_cache
     from types import SimpleNamespace
 
     from ako_amd.dispatcher import hardware
 
     arch, cus, clock, mem = _PARTS[part]
-    props = SimpleNamespace(name="AMD Radeon Graphics", major=9, minor=5, total_memory=mem,
+    props = SimpleNamespace(name=name, major=9, minor=5, total_memory=mem,
                             multi_processor_count=cus, gcnArchName=arch, L2_cache_size=4 << 20,
                             regs_per_multiprocessor=524288, shared_memory_per_block=65536)
-    ident = {"name": "AMD Radeon Graphics", "arch": arch, "cus": str(cus), "clock_khz": str(clock),
+    ident = {"name": name, "arch": arch, "cus": str(cus), "clock_khz": str(clock),
              "mem_bytes": str(mem), "hip_driver": "70226015"}
     monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
     monkeypatch.setattr(torch.cuda, "get_device_properties", lambda i: props)
@@ -250,6 +251,22 @@ def test_driver_label_prefers_the_module_version() -> None:
     assert driver_label(None, None) is None
     assert part_label("AMD Instinct MI355X", "gfx950:xnack-", 256, 2_400_000, None) == \
         "AMD Instinct MI355X gfx950 256CU 2400MHz"
+    # An empty name and the generic one describe the same part: one label, one cache key.
+    generic = {part_label(n, "gfx950:sramecc+:xnack-", 256, 2_400_000, 288 << 30)
+               for n in ("", "  ", "AMD Radeon Graphics", "AMD GPU")}
+    assert generic == {"AMD Radeon Graphics gfx950 256CU 2400MHz 288GB"}
+
+
+def test_empty_hip_name_keeps_the_generic_cache_key(monkeypatch) -> None:
+    """A box whose HIP runtime reports an empty device name finds the
+    selections cached under the generic name for the same part."""
+    hardware = _fake_rocm_device(monkeypatch, "mi355x")
+    generic = hardware.get_device_info("cuda:0").cache_key
+    for library in (True, False):
+        hardware = _fake_rocm_device(monkeypatch, "mi355x", library=library, name="")
+        key = hardware.get_device_info("cuda:0").cache_key
+        assert key == (generic if library else "AMD_Radeon_Graphics_gfx950_256CU_288GB_0")
+    hardware.clear_device_cache()
 
 
 def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
