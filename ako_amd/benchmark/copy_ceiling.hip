@@ -16,7 +16,8 @@
 // Buffers rotate through a 2 GiB source pool and a 2 GiB destination pool, so
 // consecutive launches never find their data in the 256 MB MALL or the L2s.
 // The 25 launches of a size are queued back to back, each between its own
-// pair of events, and the stream is synchronised once at the end (as
+// pair of events, behind a short spin kernel that keeps the device busy while
+// they are queued, and the stream is synchronised once at the end (as
 // bench.py times each launch), so the host's launch latency is not counted;
 // the median of the last 22 is reported as "us". The same 22 launches are
 // then queued again between one pair of events around all of them (as
@@ -59,6 +60,16 @@ __global__ __launch_bounds__(BLOCK) void copy_packets(const u32x4* __restrict__ 
   }
 }
 
+// Keeps one wavefront busy for `cycles` shader-clock cycles, with no memory
+// traffic: queued ahead of a timed region so that its first event is reached
+// with the first timed launch already queued (on an idle device the event
+// completes at once and the host's submission time of the first launch
+// would be timed). The loop ends once the clock has advanced that far.
+__global__ void spin(long long cycles) {
+  const long long t0 = clock64();
+  while (clock64() - t0 < cycles) __builtin_amdgcn_s_sleep(1);
+}
+
 static constexpr long kPool = 1L << 31;
 static constexpr double kPeakGBs = 8000.0;
 
@@ -86,6 +97,7 @@ int main(int argc, char** argv) {
   CHECK(hipMemset(src, 1, kPool));
   CHECK(hipMemset(dst, 0, kPool));
   constexpr int kReps = 25, kWarm = 3;
+  constexpr long long kLeadCycles = 200000;  // 80-140 us at MI355X clocks
   hipEvent_t start[kReps], stop[kReps];
   for (int i = 0; i < kReps; ++i) {
     CHECK(hipEventCreate(&start[i]));
@@ -108,6 +120,8 @@ int main(int argc, char** argv) {
         if (variant == 3) hipLaunchKernelGGL((copy_packets<1024, 1>), grid, dim3(1024), 0, 0, a, b, n);
         CHECK(hipGetLastError());
       };
+      hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, 0, kLeadCycles);
+      CHECK(hipGetLastError());
       for (int rep = 0; rep < kReps; ++rep) {
         CHECK(hipEventRecord(start[rep]));
         launch(rep);
@@ -115,6 +129,8 @@ int main(int argc, char** argv) {
       }
       CHECK(hipDeviceSynchronize());
       // Back to back: the timed launches again, one event pair around them all.
+      hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, 0, kLeadCycles);
+      CHECK(hipGetLastError());
       CHECK(hipEventRecord(start[0]));
       for (int rep = kWarm; rep < kReps; ++rep) launch(rep);
       CHECK(hipEventRecord(stop[0]));

@@ -122,6 +122,23 @@ class LaunchStats:
         }
 
 
+# Spin cycles queued ahead of a timed region (torch's clock-bounded spin
+# kernel, one wavefront, no memory traffic): 200k cycles are 80-140 us at the
+# clocks MI355X runs, longer than the host needs to queue the first timed
+# event and launch behind it.
+_LEAD_CYCLES = 200_000
+
+
+def queue_lead() -> None:
+    """Keep the device busy while the host queues a timed region. Recorded on
+    an idle device, the region's first event completes at once, and the
+    host's time to submit the first launch behind it is counted as device
+    time (a few to tens of microseconds, seen as an outlier on the first of a
+    run of per-launch timings). With this spin queued first, the first event
+    is reached with the first timed launch already queued behind it."""
+    torch.cuda._sleep(_LEAD_CYCLES)
+
+
 def time_steps(calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int) -> float:
     """Milliseconds for ``steps`` back-to-back passes over ``calls``, bracketed by
     one pair of events (no per-launch events inside, so nothing but the
@@ -147,6 +164,7 @@ def time_each_launch(
     marks = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in calls] for _ in range(steps)]
     torch.cuda.synchronize()
+    queue_lead()
     for step in range(steps):
         for (_, _, fn), (ev0, ev1) in zip(calls, marks[step]):
             ev0.record(stream)
@@ -186,6 +204,7 @@ def time_graph_replay(fn: Callable[[], Any], *, launches: int = 64, replays: int
     graph.replay()
     torch.cuda.synchronize()
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    queue_lead()
     begin.record()
     for _ in range(replays):
         graph.replay()
@@ -202,6 +221,7 @@ def time_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int) -> flo
     stream = torch.cuda.current_stream()
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    queue_lead()
     begin.record(stream)
     for i in range(launches):
         fns[i % len(fns)]()
@@ -279,6 +299,7 @@ def _time_replays(graph: "torch.cuda.CUDAGraph", replays: int) -> float:
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     graph.replay()
     torch.cuda.synchronize()
+    queue_lead()
     begin.record()
     for _ in range(replays):
         graph.replay()
