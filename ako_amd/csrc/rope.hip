@@ -69,11 +69,17 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   // Wavefront w of this launch rotates head chunk (w % chunks) of token
   // token0 + w / chunks. All index arithmetic is 32-bit (the host splits
   // launches so that w < 2^24 and validates batch * seq < 2^31).
+  // Spare wavefronts of the last workgroup and lanes past the last head group
+  // are not sent away early: they compute clamped, valid addresses and skip
+  // their loads and stores. With no return ahead of them, every kernel
+  // argument can be fetched at once at the start instead of one scalar load
+  // round trip after another.
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = static_cast<int>(blockIdx.x) * TPB + static_cast<int>(threadIdx.x) / kWave;
-  const int tl = wave / a.chunks;
-  if (tl >= a.tokens) return;  // no barriers below: early exit is safe
-  const int chunk = wave - tl * a.chunks;
+  const int tl_any = wave / a.chunks;
+  const bool live = tl_any < a.tokens;
+  const int tl = live ? tl_any : 0;
+  const int chunk = live ? wave - tl * a.chunks : 0;
   const int token = a.token0 + tl;
   const int half = a.head_dim / 2;
   const int unit = NEOX ? half : a.head_dim;  // elements one lane group covers
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
     hl = lane / per_unit;
     heads_per_iter = kWave / per_unit;
   }
-  if (hl >= heads_per_iter) return;
+  const bool lane_live = live && hl < heads_per_iter;
 
   const int b = token / a.seq;
   const int s = token - b * a.seq;
@@ -123,7 +129,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   for (int it = 0; it < ITERS; ++it) {
     const int h = base + it * heads_per_iter + hl;
     dst[it] = nullptr;
-    if (h < total && !(CACHE && dropped && h >= a.t0.heads)) {
+    if (lane_live && h < total && !(CACHE && dropped && h >= a.t0.heads)) {
       const bool first = h < a.t0.heads;
       const bool third = CACHE && h >= h01;
       // The tensor is chosen field by field, by value: the fields then come
