@@ -487,9 +487,11 @@ def test_rope_config3(batch: int, seq: int, dtype, table_dtype, style: str) -> N
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("style", ["neox", "interleaved"])
 @pytest.mark.parametrize("shape", [(2, 128, 8, 64), (1, 2048, 32, 128), (2, 6, 3, 8),
-                                   (2, 5, 3, 6), (1, 9, 4, 96), (3, 4, 2, 256)])
+                                   (2, 5, 3, 6), (1, 9, 4, 96), (3, 4, 2, 256), (1, 1025, 12, 96)])
 def test_rope_shapes(shape, style: str, dtype) -> None:
-    """Reference test shapes plus head dims on the scalar path (6) and odd packet counts (96)."""
+    """Reference test shapes plus head dims on the scalar path (6) and odd packet counts (96);
+    (1, 1025, 12, 96) is a four-wavefront-workgroup launch whose last workgroup holds
+    two spare wavefronts, with idle lanes in every wavefront."""
     x = grandn(shape, dtype, 12)
     cos, sin = build_rope_tables(shape[1], shape[-1], device=DEV)
     out = rope_hip(x, cos, sin, style=style)

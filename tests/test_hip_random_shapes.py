@@ -111,6 +111,8 @@ def test_rmsnorm_pipelined_random_cases(seed: int) -> None:
 
 @pytest.mark.parametrize("seed", seeds(6))
 def test_rope_random_cases(seed: int) -> None:
+    from ako_amd import _native
+
     rng = np.random.default_rng(2000 + seed)
     gen = torch.Generator(device=DEV).manual_seed(seed)
     for _ in range(10):
@@ -124,9 +126,18 @@ def test_rope_random_cases(seed: int) -> None:
         x = full[:, :, 1:h + 1]  # a strided head slice
         cos, sin = build_rope_tables(s, d, offset=offset, device=DEV)
         cos, sin = cos.to(tdtype), sin.to(tdtype)
-        case = f"b={b} s={s} h={h} d={d} {style} {dtype} tables {tdtype} offset={offset}"
-        _check(oracle.rope(to_np(x), to_np(cos), to_np(sin), style, dtype=NAMES[dtype], table_dtype=NAMES[tdtype]),
-               rope_hip(x, cos, sin, style), dtype, case)
+        # Wavefronts per workgroup (0: the default); 2-16 leave spare
+        # wavefronts in the last workgroup, which must write nothing.
+        per_block = int(rng.choice([0, 1, 2, 4, 8, 16]))
+        case = (f"b={b} s={s} h={h} d={d} {style} {dtype} tables {tdtype} offset={offset} "
+                f"waves/workgroup={per_block}")
+        try:
+            _native.set_tuning(1, 1, per_block)
+            _check(oracle.rope(to_np(x), to_np(cos), to_np(sin), style, dtype=NAMES[dtype],
+                               table_dtype=NAMES[tdtype]),
+                   rope_hip(x, cos, sin, style), dtype, case)
+        finally:
+            _native.set_tuning(1, 1, 0)
 
 
 @pytest.mark.parametrize("seed", seeds(4))
