@@ -44,6 +44,30 @@ struct RopeTensorDev {
   int64_t syb, sys, syh;
 };
 
+// Division by a launch-invariant divisor as a multiply-high and two shifts
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, figure 4.1), exact for every 32-bit unsigned
+// dividend: with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
+// t = mulhi(m, n), n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0).
+// It replaces the reciprocal-and-correct sequence of a runtime division on the
+// path to a wavefront's first load.
+struct FastDiv {
+  unsigned m;
+  unsigned s1, s2;
+};
+
+inline FastDiv make_fastdiv(unsigned d) {
+  unsigned l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  const uint64_t m = (uint64_t(1) << 32) * ((uint64_t(1) << l) - d) / d + 1;
+  return FastDiv{static_cast<unsigned>(m), l < 1 ? l : 1u, l > 1 ? l - 1 : 0u};
+}
+
+__device__ __forceinline__ unsigned fast_div(unsigned n, const FastDiv& f) {
+  const unsigned t = __umulhi(f.m, n);
+  return (t + ((n - t) >> f.s1)) >> f.s2;
+}
+
 struct RopeDev {
   RopeTensorDev t0, t1, t2;  // t2: copied, not rotated (KV-cache mode only)
   const int64_t* pos;        // KV-cache mode: device-side position of token s = 0
@@ -58,6 +82,7 @@ struct RopeDev {
   int pu_shift;      // log2(packets per unit) when a power of two, else -1
   int64_t st;
   int64_t total_tokens;  // batch * seq (scalar kernel)
+  FastDiv by_chunks, by_seq;  // dividers for chunks and seq (vector kernel)
 };
 
 template <typename T, typename TT, bool NEOX, int ITERS, int TPB, bool CACHE>
@@ -76,7 +101,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   // round trip after another.
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = static_cast<int>(blockIdx.x) * TPB + static_cast<int>(threadIdx.x) / kWave;
-  const int tl_any = wave / a.chunks;
+  const int tl_any = static_cast<int>(fast_div(static_cast<unsigned>(wave), a.by_chunks));
   const bool live = tl_any < a.tokens;
   const int tl = live ? tl_any : 0;
   const int chunk = live ? wave - tl * a.chunks : 0;
@@ -96,7 +121,7 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   }
   const bool lane_live = live && hl < heads_per_iter;
 
-  const int b = token / a.seq;
+  const int b = static_cast<int>(fast_div(static_cast<unsigned>(token), a.by_seq));
   const int s = token - b * a.seq;
   // Row of the tables and, in KV-cache mode, the cache slot of this token. A
   // token whose slot falls outside the cache writes no cache slot, and its q
@@ -251,6 +276,8 @@ template <typename T, typename TT, bool NEOX, int ITERS, bool CACHE, int TPB = k
 hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   const int64_t heads_per_wave = ITERS * (kWave / per_unit);
   d.chunks = static_cast<int>(ceil_div(d.t0.heads + d.t1.heads + (CACHE ? d.t2.heads : 0), heads_per_wave));
+  d.by_chunks = make_fastdiv(static_cast<unsigned>(d.chunks));
+  d.by_seq = make_fastdiv(static_cast<unsigned>(d.seq));
   d.pu_shift = (per_unit & (per_unit - 1)) == 0 ? __builtin_ctzll(per_unit) : -1;
   const int64_t tokens_per_launch = std::max<int64_t>(1, kWavesPerLaunch / d.chunks);
   for (int64_t first = 0; first < d.total_tokens; first += tokens_per_launch) {
