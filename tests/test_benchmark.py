@@ -4,9 +4,9 @@ graph capture fallbacks, regression diffs, roofline arithmetic."""
 from __future__ import annotations
 
 import json
-
 import random
 import statistics
+import time
 
 import pytest
 import torch
@@ -197,13 +197,18 @@ def test_ring_state_and_percentile() -> None:
 
 
 def test_compare_paired_sees_a_real_difference() -> None:
-    x, w = torch.randn(64, 4096), torch.ones(4096)
+    # Sleeps rather than compute: a sleep only ever overshoots, so the 8:1
+    # ratio cannot collapse under load from other processes on the host (a
+    # compute-bound pair with a 4:1 ratio once measured under 2x there).
+    x, w = torch.randn(4, 8), torch.ones(8)
 
     def slow(a, b):
-        for _ in range(4):
-            rmsnorm_ref(a, b)
+        time.sleep(0.008)
 
-    out = compare_paired(slow, rmsnorm_ref, (x, w), pairs=5, warmup=1, repeats=4)
+    def fast(a, b):
+        time.sleep(0.001)
+
+    out = compare_paired(slow, fast, (x, w), pairs=5, warmup=1, repeats=4)
     assert out["speedup_median"] > 2.0 and out["significant"]
     assert out["speedup_ci95"][0] <= out["speedup_median"] <= out["speedup_ci95"][1]
 
