@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fastdiv.h"
+
 namespace ako {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -17,25 +19,10 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
-// Division by a launch-invariant divisor as a multiply-high and two shifts
-// (Granlund and Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994, figure 4.1), exact for every 32-bit unsigned
-// dividend: with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
-// t = mulhi(m, n), n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0).
-// It replaces the reciprocal-and-correct sequence of a runtime division on the
-// path to a wavefront's first load. make_fastdiv runs on the host.
-struct FastDiv {
-  unsigned m;
-  unsigned s1, s2;
-};
-
-inline FastDiv make_fastdiv(unsigned d) {
-  unsigned l = 0;
-  while ((uint64_t(1) << l) < d) ++l;
-  const uint64_t m = (uint64_t(1) << 32) * ((uint64_t(1) << l) - d) / d + 1;
-  return FastDiv{static_cast<unsigned>(m), l < 1 ? l : 1u, l > 1 ? l - 1 : 0u};
-}
-
+// Division by a launch-invariant divisor (FastDiv, built on the host by
+// make_fastdiv): a multiply-high and two shifts, exact for every 32-bit
+// unsigned dividend, instead of the reciprocal-and-correct sequence of a
+// runtime division on the path to a wavefront's first load.
 __device__ __forceinline__ unsigned fast_div(unsigned n, const FastDiv& f) {
   const unsigned t = __umulhi(f.m, n);
   return (t + ((n - t) >> f.s1)) >> f.s2;
