@@ -216,6 +216,7 @@ def time_graph_replay(fn: Callable[[], Any], *, launches: int = 64, replays: int
     torch.cuda.synchronize()
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     queue_lead()
+    graph.replay()  # untimed, ahead of the first event: the timed replays follow the same work
     begin.record()
     for _ in range(replays):
         graph.replay()
@@ -228,11 +229,16 @@ def time_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int) -> flo
     """Mean device milliseconds per call over ``launches`` back-to-back calls
     cycling through ``fns`` (independent input copies), one event pair around
     the whole loop: for kernels short enough that per-launch events would
-    distort them."""
+    distort them. One untimed cycle through ``fns`` is queued ahead of the
+    first event (after the spin lead), so the timed calls continue a cycle
+    already running: every call still finds its inputs cold, and the device
+    is at its loaded clocks from the first timed call on."""
     stream = torch.cuda.current_stream()
     begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     queue_lead()
+    for fn in fns:
+        fn()
     begin.record(stream)
     for i in range(launches):
         fns[i % len(fns)]()
@@ -311,6 +317,7 @@ def _time_replays(graph: "torch.cuda.CUDAGraph", replays: int) -> float:
     graph.replay()
     torch.cuda.synchronize()
     queue_lead()
+    graph.replay()  # untimed, ahead of the first event: the timed replays follow the same work
     begin.record()
     for _ in range(replays):
         graph.replay()
