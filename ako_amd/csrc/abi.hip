@@ -168,6 +168,11 @@ int ako_set_tuning(int op, int key, int value) {
         ako::g_rms_tuning.load_groups = value;
         return AKO_OK;
       }
+      if (key == 12) {
+        if (value > 2) return fail(AKO_ERR_INVALID_ARGUMENT, "write-through stores must be 0, 1 or 2");
+        ako::g_rms_tuning.write_through = value;
+        return AKO_OK;
+      }
       break;
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }

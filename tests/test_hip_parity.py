@@ -297,6 +297,57 @@ def test_rmsnorm_residual_load_groups_match(dtype, w_dtype) -> None:
         _native.set_tuning(0, 11, 0)
 
 
+# (dtype, weight dtype, hidden, row stride or None): rows on the (16, 2) shape,
+# full (16384 half / 8192 fp32 elements) and with idle lanes (9000, 12000).
+WRITE_THROUGH_CASES = [
+    (torch.float16, torch.float16, 16384, None),
+    (torch.bfloat16, torch.float32, 16384, 16448),
+    (torch.float16, torch.float16, 12000, None),
+    (torch.bfloat16, torch.bfloat16, 9000, 9008),
+    (torch.float32, torch.float32, 8192, None),
+]
+
+
+@pytest.mark.parametrize("dtype,w_dtype,h,stride", WRITE_THROUGH_CASES)
+def test_rmsnorm_write_through_stores_match(dtype, w_dtype, h, stride) -> None:
+    """Rows on the (16, 2) shape stored write-through (key 12 = 2, buffer
+    stores with sc1 nt on a resource covering the row) and with plain
+    non-temporal stores (key 12 = 1), residual rows with either load grouping:
+    the same values in the same places, so bit-identical outputs, also where
+    lanes sit idle and where input rows are padded; the default
+    (write-through from 257 rows) against the oracle on sampled rows."""
+    from ako_amd import _native
+
+    try:
+        for rows in (3, 300):
+            width = stride or h
+            xb = grandn((rows, width), dtype, 70 + rows)
+            rb = grandn((rows, width), dtype, 71 + rows)
+            x, r = xb[:, :h], rb[:, :h]
+            w = grandn((h,), w_dtype, 72, scale=0.1, shift=1.0)
+            outs = {}
+            for wt in (1, 2, 0):
+                for groups in (1, 2):
+                    _native.set_tuning(0, 12, wt)
+                    _native.set_tuning(0, 11, groups)
+                    outs[(wt, groups)] = (rmsnorm_hip(x, w), *rmsnorm_residual_hip(x, r, w))
+            base = outs[(1, 1)]
+            for key, got in outs.items():
+                assert all(torch.equal(a, b) for a, b in zip(got, base)), (rows, key)
+            idx = sample_rows(rows, 64)
+            sel = torch.as_tensor(idx, device=DEV)
+            wname = NAMES[w_dtype]
+            assert_oracle(oracle.rmsnorm(to_np(x[sel]), to_np(w), dtype=NAMES[dtype], w_dtype=wname),
+                          to_np(outs[(0, 1)][0][sel]), dtype)
+            ey, es = oracle.rmsnorm_residual(to_np(x[sel]), to_np(r[sel]), to_np(w), dtype=NAMES[dtype],
+                                             w_dtype=wname)
+            np.testing.assert_array_equal(to_np(outs[(0, 1)][2][sel]), es)
+            assert_oracle(ey, to_np(outs[(0, 1)][1][sel]), dtype)
+    finally:
+        _native.set_tuning(0, 11, 0)
+        _native.set_tuning(0, 12, 0)
+
+
 # (dtype, weight dtype, hidden, forced (waves per row, packets per lane) or None).
 # Every shape with a pipelined instantiation appears; None is the default shape
 # of a launch of many rows (full rows: hidden = 64 * waves * packets * E).
