@@ -25,7 +25,7 @@ struct RmsTuning {
   int early_weights = 0;    // key 8: 1 = weights after the row's loads return, 2 = with them (0 = by launch size)
   int pipeline = 0;         // key 9: 1 = never the pipelined persistent kernel, 2 = whenever eligible (0 = heuristic)
   int pipe_blocks_per_cu = 0;  // key 10: workgroups per CU in the pipelined grid (0 = 16 wavefronts per CU)
-  int load_groups = 0;      // key 11: residual (16, 2) rows: 1 = both packets per load group, 2 = one (0 = by dtype)
+  int load_groups = 0;      // key 11: residual (16, 2) rows: 1 = both packets per load group, 2 = one (0 = one with write-through stores, else by dtype)
   int write_through = 0;    // key 12: (16, 2) rows: 1 = non-temporal stores, 2 = write-through stores (0 = by launch size)
 };
 struct RopeTuning {

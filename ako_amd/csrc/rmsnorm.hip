@@ -690,12 +690,12 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
                      a.hidden * static_cast<int64_t>(sizeof(T)) <= kEarlyWeightRowBytes);
     if (ew) return run_reg_launch<T, W, WPR, VPT, RES, true>(a, stream);
   }
-  // One packet per load group for bf16 residual rows of 16 wavefronts x 2
-  // packets (rows of 8193-16384 elements), launches of many rows.
-  // Medians of 10 interleaved repetitions on MI355X, 16384 x 16384, cold inputs:
-  // bf16 +1.5% back to back and +1.9% per launch (two separate runs: +1.5 to
-  // +1.9%); fp16 -0.3%, so fp16 keeps whole groups, as do plain rows (-1.4%
-  // bf16, -3.5% fp16).
+  // Without write-through stores (key 12 = 1): one packet per load group for
+  // bf16 residual rows of 16 wavefronts x 2 packets in launches of many rows.
+  // Medians of 10 interleaved repetitions on MI355X, 16384 x 16384, cold
+  // inputs, non-temporal stores: bf16 +1.5% back to back and +1.9% per launch;
+  // fp16 -0.3%, so fp16 keeps whole groups, as do plain rows (-1.4% bf16,
+  // -3.5% fp16).
   // Rows of 8193-16384 elements at 16 wavefronts x 2 packets in launches of
   // many rows store write-through (see store_write_through); residual rows
   // then take one packet per load group, fp16 and bf16 alike.
