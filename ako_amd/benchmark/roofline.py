@@ -247,6 +247,18 @@ def time_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int) -> flo
     return begin.elapsed_time(end) / launches
 
 
+def settled_back_to_back(fns: Sequence[Callable[[], Any]], *, launches: int, discard: int = 2,
+                         keep: int = 3) -> float:
+    """The median of ``keep`` ``time_back_to_back`` timings, after ``discard``
+    more whose results are dropped. Right after a cell's inputs are
+    allocated, the first 60-launch timings of MI355X read low and settle over
+    the next two or three (residual RMSNorm 16384 x 8192: 79.7%, 80.5%, then
+    80.7-80.8% of peak); the discarded runs cover that."""
+    for _ in range(discard):
+        time_back_to_back(fns, launches=launches)
+    return statistics.median(time_back_to_back(fns, launches=launches) for _ in range(keep))
+
+
 def parse_copy_ceiling(text: str) -> dict[str, Any] | None:
     """The fastest block shape among the JSON lines printed by ``copy_ceiling``
     for one size (None when there are none)."""

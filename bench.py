@@ -164,7 +164,7 @@ def headline_back_to_back(torch, rf, dev, rnd) -> dict[str, float]:
                 for fn in fns:
                     fn()
                 name = f"rmsnorm{'_residual' if residual else ''}_{tag}_{RMS_ROWS}x{h}"
-                out[name] = sorted(rf.time_back_to_back(fns, launches=60) for _ in range(3))[1]
+                out[name] = rf.settled_back_to_back(fns, launches=60)
                 del sets, fns
                 torch.cuda.empty_cache()
     return out
@@ -280,9 +280,9 @@ def time_extras(cells, torch, rf, peak, ceilings):
         if decode:
             ms = rf.time_back_to_back(fns[:1], launches=60)  # hot: one input, as before
         else:
-            # Median of three: single 60-launch timings of these 8-220 us
-            # launches move by several percent from one to the next.
-            ms = sorted(rf.time_back_to_back(fns, launches=60) for _ in range(3))[1]
+            # Median of three settled timings: single 60-launch timings of
+            # these 8-220 us launches move by several percent from one to the next.
+            ms = rf.settled_back_to_back(fns, launches=60)
         stats = rf.LaunchStats(name, nbytes, [ms])
         row = stats.to_dict(peak)
         row.pop("launches")
