@@ -145,7 +145,8 @@ def headline_back_to_back(torch, rf, dev, rnd) -> dict[str, float]:
     """Each cell of the step on its own: mean ms per launch over 60 launches
     queued back to back between one event pair, cycling through enough input
     copies that every launch reads cold data (no per-launch events, whose
-    1.5-2 us would be counted in the launch); the median of three such runs."""
+    1.5-2 us would be counted in the launch); the median of three such runs
+    after two discarded ones (``roofline.settled_back_to_back``)."""
     from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
 
     out = {}
