@@ -289,6 +289,35 @@ def to_markdown(result: dict[str, Any], command: str) -> str:
     return "\n".join(lines)
 
 
+def launch_window(rows: list[tuple[str, int, int]], name_filter: str, first: int, count: int) -> dict[str, Any]:
+    """Durations of launches ``first .. first + count - 1`` (0-based, in start
+    order) of the one kernel whose name contains ``name_filter``: the launches
+    a benchmark timed with its own events, to set the two clocks side by side."""
+    names = {name for name, _, _ in rows if name_filter in name}
+    if len(names) != 1:
+        raise ValueError(f"--window {name_filter!r} matches {len(names)} kernels, expected one")
+    (name,) = names
+    durs = [(end - start) / 1e3 for n, start, end in rows if n == name]
+    if first + count > len(durs):
+        raise ValueError(f"--window asks for launches {first}..{first + count - 1} of {name}, "
+                         f"the trace holds {len(durs)}")
+    win = durs[first:first + count]
+    return {"name": name, "first": first, "count": count, "launches_in_trace": len(durs),
+            "mean_us": round(statistics.fmean(win), 2), "median_us": round(statistics.median(win), 2),
+            "min_us": round(min(win), 2), "max_us": round(max(win), 2)}
+
+
+def window_markdown(win: dict[str, Any], events_us: float | None) -> str:
+    text = (f"Launches {win['first']}-{win['first'] + win['count'] - 1} (0-based, of {win['launches_in_trace']}) "
+            f"of `{win['name'][:90]}...`, the {win['count']} that bench.py timed with an event pair each "
+            f"(`roofline.event_launches`): mean {win['mean_us']:.2f} us, median {win['median_us']:.2f} us, "
+            f"min {win['min_us']:.2f} us, max {win['max_us']:.2f} us by kernel duration")
+    if events_us is not None:
+        text += (f"; the same launches by the events of the same run: mean {events_us:.2f} us "
+                 f"(`roofline.mean_launch_us`), {100 * (events_us / win['mean_us'] - 1):+.1f}%")
+    return text + ".\n"
+
+
 def stats_markdown(rows: list[dict[str, Any]], command: str, title: str, top: int = 40) -> str:
     lines = [f"# {title}", "", "Command:", "", "```", command, "```", "",
              "| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---:|---:|---:|---:|---:|"]
@@ -324,6 +353,11 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--command", default="")
     ap.add_argument("--md", type=Path, required=True)
     ap.add_argument("--json", type=Path, help="also write the figures as JSON (e.g. next to a BenchmarkReport)")
+    ap.add_argument("--window", default=None, metavar="SUBSTR:FIRST:COUNT",
+                    help="with --stats and --trace: kernel durations of launches FIRST..FIRST+COUNT-1 of "
+                         "the kernel whose name contains SUBSTR")
+    ap.add_argument("--bench-json", type=Path, default=None,
+                    help="with --window: the bench.py line of the same run, for its event timing")
     args = ap.parse_args(argv)
     if args.pmc:
         cells = counters_by_cell(args.pmc, args.manifest)
@@ -334,15 +368,27 @@ def main(argv: list[str] | None = None) -> int:
         groups = [g for g in groups if name_matches(g["name"], args.filter)]
         args.md.write_text(grid_markdown(groups, args.command, args.title, args.note))
         record = {"kind": "durations_by_grid", "title": args.title, "groups": groups}
-    elif args.trace:
+    elif args.trace and not args.stats:
         result = tail_breakdown(read_kernel_trace(args.trace), args.steps, tail_ms=args.tail_ms,
                                 marker=args.marker)
         args.md.write_text(breakdown_markdown(result, args.command, args.title))
         record = {"kind": "trace_tail_breakdown", "title": args.title, **result}
     elif args.stats:
         rows = read_kernel_stats(args.stats)
-        args.md.write_text(stats_markdown(rows, args.command, args.title))
+        text = stats_markdown(rows, args.command, args.title)
         record = {"kind": "kernel_stats", "title": args.title, "kernels": rows}
+        if args.window:
+            if not args.trace:
+                ap.error("--window needs --trace")
+            substr, first, count = args.window.rsplit(":", 2)
+            win = launch_window(read_kernel_trace(args.trace), substr, int(first), int(count))
+            events_us = None
+            if args.bench_json:
+                line = args.bench_json.read_text().strip().splitlines()[-1]
+                events_us = json.loads(line)["roofline"]["mean_launch_us"]
+            text += "\n" + window_markdown(win, events_us)
+            record["window"] = {**win, "events_mean_us": events_us}
+        args.md.write_text(text)
     else:
         result = traffic(args.fetch, args.write, args.manifest)
         args.md.write_text(to_markdown(result, args.command))

@@ -155,8 +155,12 @@ def time_steps(calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: in
     return begin.elapsed_time(end)
 
 
+#: Untimed passes that ``time_each_launch`` queues ahead of its timed ones.
+LEAD_PASSES = 3
+
+
 def time_each_launch(
-    calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int, lead_passes: int = 3
+    calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int, lead_passes: int = LEAD_PASSES
 ) -> list[LaunchStats]:
     """Per-launch device durations: an event pair around every launch of
     ``steps`` passes over ``calls`` (name, alg_bytes, thunk).

@@ -461,6 +461,11 @@ def main() -> int:
         "mean_launch_us": round(dominant.mean_ms * 1e3, 2),
         "launches_timed": len(dominant.durations_ms),
         "timing": "HIP events around each launch on the launch stream, over the same K steps as value",
+        # Which launches of this kernel (0-based, counted over the process) carry
+        # the event pairs: after the warm-up passes, the K steps of `value` and
+        # the lead passes. A kernel trace of the same run can be cut to exactly
+        # these (python -m ako_amd.benchmark.rocprof --window).
+        "event_launches": {"first": args.warmup + args.steps + rf.LEAD_PASSES, "count": args.steps},
     }
     if args.traffic.exists():
         from ako_amd.benchmark.rocprof import load_traffic_md

@@ -95,6 +95,41 @@ def test_kernel_stats_and_trace_tail(tmp_path) -> None:
         rocprof.tail_breakdown(rows, 9, marker="norm")
 
 
+def test_launch_window_cuts_the_event_timed_launches(tmp_path) -> None:
+    """``--window`` averages exactly launches FIRST..FIRST+COUNT-1 of one kernel,
+    counted in start order over that kernel alone, and sets the bench line's
+    event figure beside them."""
+    trace = tmp_path / "t.csv"
+    with open(trace, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        t = 0
+        for i in range(10):  # norm launch i lasts (i + 1) us; another kernel in between
+            w.writerow({"Kernel_Name": "ako::norm<bf16>", "Start_Timestamp": t, "End_Timestamp": t + 1000 * (i + 1)})
+            w.writerow({"Kernel_Name": "ako::norm<fp16>", "Start_Timestamp": t + 20_000, "End_Timestamp": t + 90_000})
+            t += 100_000
+    rows = rocprof.read_kernel_trace(trace)
+    win = rocprof.launch_window(rows, "norm<bf16>", 4, 3)  # launches 4, 5, 6: 5, 6, 7 us
+    assert (win["mean_us"], win["median_us"], win["min_us"], win["max_us"]) == (6.0, 6.0, 5.0, 7.0)
+    assert win["launches_in_trace"] == 10
+    with pytest.raises(ValueError, match="matches 2 kernels"):
+        rocprof.launch_window(rows, "norm", 0, 1)
+    with pytest.raises(ValueError, match="holds 10"):
+        rocprof.launch_window(rows, "norm<bf16>", 8, 3)
+
+    stats = tmp_path / "s.csv"
+    stats.write_text('"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"\n'
+                     '"ako::norm<bf16>",10,55000,5500.0,50.0,1000,10000,5.0\n')
+    bench = tmp_path / "b.json"
+    bench.write_text("noise\n" + json.dumps({"roofline": {"mean_launch_us": 6.6}}) + "\n")
+    md = tmp_path / "o.md"
+    assert rocprof.main(["--stats", str(stats), "--trace", str(trace), "--window", "norm<bf16>:4:3",
+                         "--bench-json", str(bench), "--md", str(md)]) == 0
+    text = md.read_text()
+    assert "Launches 4-6 (0-based, of 10)" in text and "mean 6.00 us" in text
+    assert "mean 6.60 us (`roofline.mean_launch_us`), +10.0%" in text
+
+
 def test_counters_by_cell_averages_each_cell(tmp_path) -> None:
     manifest = {"dispatches": [{"cell": "a", "alg_bytes": 1}, {"cell": "a", "alg_bytes": 1},
                                {"cell": "b", "alg_bytes": 1}]}
