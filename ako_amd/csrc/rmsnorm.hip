@@ -621,6 +621,14 @@ RegShape pick_shape(int64_t nvec, bool residual, int64_t rows) {
 }
 
 constexpr unsigned kXcdChunk = 8;
+// Residual rows of 16384 half elements (the one-workgroup-per-CU launches
+// below, write-through stores, one packet per load group) take runs of 16.
+// Medians of 9 rotating back-to-back runs on MI355X, same buffers, outputs
+// identical: runs of 16 read 81.5% (bf16) and 82.7% (fp16) of peak against
+// 80.3% and 81.3% with runs of 8; runs of 12, 20, 24 and 32 were no better
+// than 8. Plain rows of 16384 and residual rows of 8192 showed no consistent
+// gain from 16 (within +-0.5 points) and keep 8.
+constexpr unsigned kXcdChunkWideResidual = 16;
 
 // Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
 // the dispatch packet never wraps; larger problems take several launches,
@@ -642,11 +650,13 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   // such rows per CU exceed the CU's share of its XCD's L2 (4 MiB / 32 CUs),
   // so an LDS reservation above half the CU's 160 KiB limits those launches to
   // one 16-wavefront workgroup per CU (measured +1-3% at 16384 x 16384).
+  const bool one_per_cu = RES && WPR == 16 && a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024;
   unsigned lds = static_cast<unsigned>(g_rms_tuning.lds_reserve);
-  if (lds == 0 && RES && WPR == 16 && a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024)
-    lds = 82 * 1024;
+  if (lds == 0 && one_per_cu) lds = 82 * 1024;
+  const unsigned run = one_per_cu && VPT == 2 && sizeof(T) == 2 ? kXcdChunkWideResidual : kXcdChunk;
   // Default: rows of >= 16 KiB go to the XCDs in runs of 8 consecutive rows
-  // (once the launch holds 8 such runs); narrower rows keep block order.
+  // (16 for the residual rows of 16384 half elements; once the launch holds 8
+  // such runs); narrower rows keep block order.
   // Medians of 5 cold runs on MI355X, 16384 rows, fp16/bf16, against block
   // order: +1% at 16 KiB rows, +4% (plain) and +8-10% (residual) at 32 KiB
   // rows, -1-2% at 8 KiB rows; whole-grid runs (chunk = n / 8) lose up to 12%
@@ -654,7 +664,7 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   const bool wide = a.hidden * static_cast<int64_t>(sizeof(T)) >= 16 * 1024;
   for (int64_t b0 = 0; b0 < total_blocks; b0 += cap) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, total_blocks - b0)));
-    unsigned xcd_chunk = wide && grid.x >= 8 * kXcdChunk ? kXcdChunk : 1;
+    unsigned xcd_chunk = !wide ? 1u : grid.x >= 8 * run ? run : grid.x >= 8 * kXcdChunk ? kXcdChunk : 1u;
     if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
     if (g_rms_tuning.row_order == 2)
       xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
