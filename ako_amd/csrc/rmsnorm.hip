@@ -623,11 +623,12 @@ RegShape pick_shape(int64_t nvec, bool residual, int64_t rows) {
 constexpr unsigned kXcdChunk = 8;
 // Residual rows of 16384 half elements (the one-workgroup-per-CU launches
 // below, write-through stores, one packet per load group) take runs of 16.
-// Medians of 9 rotating back-to-back runs on MI355X, same buffers, outputs
-// identical: runs of 16 read 81.5% (bf16) and 82.7% (fp16) of peak against
-// 80.3% and 81.3% with runs of 8; runs of 12, 20, 24 and 32 were no better
-// than 8. Plain rows of 16384 and residual rows of 8192 showed no consistent
-// gain from 16 (within +-0.5 points) and keep 8.
+// Medians of 7-10 rotating back-to-back runs on MI355X, same buffers, outputs
+// identical, three boxes: runs of 16 gained 0.4-1.4 points of peak over runs
+// of 8 (e.g. 81.5% / 82.7% against 80.3% / 81.3%, bf16 / fp16); runs of 12,
+// 20, 24 and 32 were no better than 8, and the whole 12-launch step read
+// 6542 against 6525 GB/s. Plain rows of 16384 and residual rows of 8192
+// showed no consistent gain from 16 and keep 8.
 constexpr unsigned kXcdChunkWideResidual = 16;
 
 // Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
