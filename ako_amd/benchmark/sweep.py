@@ -112,6 +112,7 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
     wins = total = decode_total = decode_wins = 0
     others: list[dict[str, Any]] = []
     leads: dict[str, list[float]] = {}
+    worst_ulps: dict[str, float] = {}
     for op, shape, dtype, tensors, kw in cells(ops, device):
         if keep is not None and not keep(op, shape, dtype):
             continue
@@ -138,6 +139,8 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
             latencies_ms={k: round(v, 5) for k, v in lat.items()},
             rejected=list(result.rejected),
         )
+        if hip_report is not None and hip_report.get("err_ulps") is not None:
+            worst_ulps[op] = max(worst_ulps.get(op, 0.0), float(hip_report["err_ulps"]))
         hip_won = result.entry.backend == "hip"
         total += 1
         wins += int(hip_won)
@@ -164,6 +167,9 @@ def run(out_dir: Path, ops: set[str], *, warmup: int = 5, repeats: int = 20,
                # The reference campaign's headline numbers (scripts/run_campaign.py:287-337):
                # the selected kernel's median lead over the fastest baseline, per op and phase.
                "median_lead_vs_best_baseline": {k: round(statistics.median(v), 3) for k, v in sorted(leads.items())},
+               # The HIP candidate's largest error over each op's cells, in ulps
+               # of the reference output's largest magnitude (the gate's report).
+               "max_err_ulps": {k: round(v, 3) for k, v in sorted(worst_ulps.items())},
                "not_hip": others, "gpu": info.device_name, "cache_key": info.cache_key}
     (out_dir / "selection_summary.json").write_text(json.dumps(summary, indent=2))
     return summary

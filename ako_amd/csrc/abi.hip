@@ -15,10 +15,6 @@
 #include "ako_hip.h"
 #include "launch.h"
 
-#ifndef AKO_RMS_NT
-#define AKO_RMS_NT 1
-#endif
-
 namespace {
 
 thread_local std::string g_last_error;
@@ -103,8 +99,7 @@ int ako_hip_runtime_version(void) {
 
 const char* ako_build_info(void) {
   static const std::string info = std::string("ako_hip abi=") + std::to_string(AKO_ABI_VERSION) +
-                                  " arch=gfx950 hip_headers=" + std::to_string(HIP_VERSION) +
-                                  " rms_nontemporal=" + std::to_string(AKO_RMS_NT);
+                                  " arch=gfx950 hip_headers=" + std::to_string(HIP_VERSION);
   return info.c_str();
 }
 

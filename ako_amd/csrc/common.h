@@ -111,13 +111,9 @@ __device__ __forceinline__ void load_f32(const T* p, float (&out)[N]) {
 // nothing from v_dot2, so it keeps the FMA chain.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-#ifndef AKO_SUMSQ_DOT2
-#define AKO_SUMSQ_DOT2 1
-#endif
-
 template <typename T, int N>
 __device__ __forceinline__ float sumsq_add(const Pack<T, N>& p, float acc) {
-  if constexpr (AKO_SUMSQ_DOT2 && __is_same(T, __bf16) && Pack<T, N>::kBytes == 16) {
+  if constexpr (__is_same(T, __bf16) && Pack<T, N>::kBytes == 16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bf16x2 h = __builtin_bit_cast(bf16x2, static_cast<unsigned>(p.raw[i]));

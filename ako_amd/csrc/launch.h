@@ -7,33 +7,39 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace ako {
 
 enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
 inline int dtype_bytes(int dt) { return dt == kF32 ? 4 : 2; }
 
-// Launch-shape overrides set through ako_set_tuning (0 = heuristic).
+// Launch-shape overrides set through ako_set_tuning (0 = heuristic). Every
+// key is an atomic int: ako_set_tuning may run on any host thread while other
+// threads launch, and each read in a launcher sees the value before or after
+// a concurrent set (a launch concurrent with several sets may mix them).
+using TuningKey = std::atomic<int>;
 struct RmsTuning {
-  int waves_per_row = 0;    // key 1
-  int vecs_per_thread = 0;  // key 2
-  int force_stream = 0;     // key 3: 1 = always use the two-pass kernel
-  int lds_reserve = 0;      // key 4: bytes of LDS reserved per workgroup (caps rows in flight per CU)
-  int row_order = 0;        // key 5: 1 = rows in block order, 2 = XCD-blocked order
-  int xcd_chunk = 0;        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
-  int max_blocks = 0;       // key 7: cap on workgroups per launch (0 = 2^31 work-items)
-  int early_weights = 0;    // key 8: 1 = weights after the row's loads return, 2 = with them (0 = by launch size)
-  int pipeline = 0;         // key 9: 1 = never the pipelined persistent kernel, 2 = whenever eligible (0 = heuristic)
-  int pipe_blocks_per_cu = 0;  // key 10: workgroups per CU in the pipelined grid (0 = 16 wavefronts per CU)
-  int load_groups = 0;      // key 11: residual (16, 2) rows: 1 = both packets per load group, 2 = one (0 = one with write-through stores, else by dtype)
-  int write_through = 0;    // key 12: (16, 2) rows: 1 = non-temporal stores, 2 = write-through stores (0 = by launch size)
+  TuningKey waves_per_row{0};    // key 1
+  TuningKey vecs_per_thread{0};  // key 2
+  TuningKey force_stream{0};     // key 3: 1 = always use the two-pass kernel
+  TuningKey lds_reserve{0};      // key 4: bytes of LDS reserved per workgroup (caps rows in flight per CU)
+  TuningKey row_order{0};        // key 5: 1 = rows in block order, 2 = XCD-blocked order
+  TuningKey xcd_chunk{0};        // key 6: consecutive blocks per XCD run in XCD-blocked order (0 = n / 8)
+  TuningKey max_blocks{0};       // key 7: cap on workgroups per launch (0 = 2^31 work-items)
+  TuningKey early_weights{0};    // key 8: 1 = weights after the row's loads return, 2 = with them (0 = by launch size)
+  TuningKey pipeline{0};         // key 9: 1 = never the pipelined persistent kernel, 2 = whenever eligible (0 = heuristic)
+  TuningKey pipe_blocks_per_cu{0};  // key 10: workgroups per CU in the pipelined grid (0 = 16 wavefronts per CU)
+  TuningKey load_groups{0};      // key 11: residual (16, 2) rows: 1 = both packets per load group, 2 = one (0 = one with write-through stores, else by dtype)
+  TuningKey write_through{0};    // key 12: (16, 2) rows: 1 = non-temporal stores, 2 = write-through stores (0 = by launch size)
 };
 struct RopeTuning {
-  int tokens_per_block = 0;  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)
-  int iters = 0;             // key 2: head chunks unrolled per loop trip
+  TuningKey tokens_per_block{0};  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)
+  TuningKey iters{0};             // key 2: head chunks unrolled per loop trip
 };
 struct SwigluTuning {
-  int vecs_per_thread = 0;  // key 1: packets per lane (1, 2, 4 or 8)
+  TuningKey vecs_per_thread{0};  // key 1: packets per lane (1, 2, 4 or 8)
 };
 extern RmsTuning g_rms_tuning;
 extern RopeTuning g_rope_tuning;

@@ -42,10 +42,6 @@
 #include "common.h"
 #include "launch.h"
 
-#ifndef AKO_RMS_PREFETCH_W
-#define AKO_RMS_PREFETCH_W 1
-#endif
-
 namespace ako {
 
 RmsTuning g_rms_tuning;
@@ -114,8 +110,8 @@ __device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, const Xc
   return full * 8 * r.chunk + x * rest + (i - full * r.chunk);
 }
 
-template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool NTL, bool NTS, bool EW,
-          bool SPLIT = false, bool WT = false>
+template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool EW, bool SPLIT = false,
+          bool WT = false>
 __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     const T* __restrict__ x, const T* __restrict__ res, const W* __restrict__ w,
     T* __restrict__ y, T* __restrict__ rout, int64_t row0, int64_t rows, int hidden, int64_t sx,
@@ -137,7 +133,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
   // dependent chain, and a norm weight that the rest of a model step has
   // evicted then costs one HBM round trip instead of a second one after x.
   static_assert(!EW || VPT <= 4, "early weights need the first group's weights in registers");
-  constexpr bool kPrefetchW = (AKO_RMS_PREFETCH_W != 0 || EW) && VPT <= 4;
+  constexpr bool kPrefetchW = VPT <= 4;
   using P = Pack<T, E>;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -163,8 +159,8 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
     for (int k = 0; k < G; ++k) {
       const int vi = t + (g0 + k) * TPR;
       if (active && vi < nvec) {
-        v[g0 + k] = load_pack<T, E, NTL>(xr + vi * E);
-        if constexpr (RES) rv[k] = load_pack<T, E, NTL>(res + row * sr + vi * E);
+        v[g0 + k] = load_pack<T, E, true>(xr + vi * E);
+        if constexpr (RES) rv[k] = load_pack<T, E, true>(res + row * sr + vi * E);
       }
     }
     if constexpr (EW) {
@@ -187,7 +183,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
           if constexpr (WT)
             store_write_through<T, E>(rout + row * srout, hidden * static_cast<int>(sizeof(T)), vi * E, v[g0 + k]);
           else
-            store_pack<T, E, NTS>(rout + row * srout + vi * E, v[g0 + k]);
+            store_pack<T, E, true>(rout + row * srout + vi * E, v[g0 + k]);
         }
         ss = sumsq_add(v[g0 + k], ss);
       }
@@ -247,7 +243,7 @@ __global__ __launch_bounds__(kWave* WPR* RPB) void rmsnorm_reg(
         if constexpr (WT)
           store_write_through<T, E>(yr, hidden * static_cast<int>(sizeof(T)), vi * E, o);
         else
-          store_pack<T, E, NTS>(yr + vi * E, o);
+          store_pack<T, E, true>(yr + vi * E, o);
       }
     }
   }
@@ -564,13 +560,6 @@ __global__ __launch_bounds__(kStreamBlock) void rmsnorm_shard_apply(
   }
 }
 
-#ifndef AKO_RMS_NT
-#define AKO_RMS_NT 1
-#endif
-#ifndef AKO_RMS_NT_STORE
-#define AKO_RMS_NT_STORE AKO_RMS_NT
-#endif
-
 namespace {
 
 // Launches of at most this many rows leave CUs without a workgroup (256 CUs).
@@ -610,10 +599,9 @@ RegShape pick_shape(int64_t nvec, bool residual, int64_t rows) {
   else if (nvec <= 1024) s = one_packet ? RegShape{16, 1} : RegShape{8, 2};
   else if (nvec <= 2048) s = {16, 2};
   else if (nvec <= 4096) s = {16, 4};
-  const RmsTuning& tu = g_rms_tuning;
-  if (tu.waves_per_row > 0 || tu.vecs_per_thread > 0) {
-    RegShape want{tu.waves_per_row > 0 ? tu.waves_per_row : s.wpr,
-                  tu.vecs_per_thread > 0 ? tu.vecs_per_thread : s.vpt};
+  const int want_wpr = g_rms_tuning.waves_per_row, want_vpt = g_rms_tuning.vecs_per_thread;
+  if (want_wpr > 0 || want_vpt > 0) {
+    RegShape want{want_wpr > 0 ? want_wpr : s.wpr, want_vpt > 0 ? want_vpt : s.vpt};
     for (const RegShape& c : kRegShapes)
       if (c.wpr == want.wpr && c.vpt == want.vpt && int64_t(c.wpr) * 64 * c.vpt >= nvec) return c;
   }
@@ -666,10 +654,10 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   for (int64_t b0 = 0; b0 < total_blocks; b0 += cap) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, total_blocks - b0)));
     unsigned xcd_chunk = !wide ? 1u : grid.x >= 8 * run ? run : grid.x >= 8 * kXcdChunk ? kXcdChunk : 1u;
-    if (g_rms_tuning.row_order == 1) xcd_chunk = 1;
-    if (g_rms_tuning.row_order == 2)
-      xcd_chunk = g_rms_tuning.xcd_chunk > 0 ? unsigned(g_rms_tuning.xcd_chunk) : unsigned(grid.x / 8);
-    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, AKO_RMS_NT != 0, AKO_RMS_NT_STORE != 0, EW, SPLIT, WT>),
+    const int order = g_rms_tuning.row_order, chunk = g_rms_tuning.xcd_chunk;
+    if (order == 1) xcd_chunk = 1;
+    if (order == 2) xcd_chunk = chunk > 0 ? unsigned(chunk) : unsigned(grid.x / 8);
+    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, EW, SPLIT, WT>),
                        grid, block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                        static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                        b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
@@ -763,8 +751,8 @@ bool pipe_shape(const RegShape& s) {
 // GB/s with 16 wavefronts per CU against 6029 with 8; residual 6976 with 8
 // against 6826 with 16.
 int64_t pipe_blocks(int wpr, bool residual, int64_t rows) {
-  const int64_t per_cu = g_rms_tuning.pipe_blocks_per_cu > 0 ? g_rms_tuning.pipe_blocks_per_cu
-                                                             : std::max(1, (residual ? 8 : 16) / wpr);
+  const int forced = g_rms_tuning.pipe_blocks_per_cu;
+  const int64_t per_cu = forced > 0 ? forced : std::max(1, (residual ? 8 : 16) / wpr);
   const int64_t blocks = std::min<int64_t>(rows, per_cu * device_cus());
   return std::max<int64_t>(8, blocks / 8 * 8);
 }
@@ -935,16 +923,13 @@ hipError_t run_shard_apply_r(const RmsShardArgs& a, hipStream_t stream) {
   return hipSuccess;
 }
 
-#ifndef AKO_TP_APPLY_ROWS
-#define AKO_TP_APPLY_ROWS 2
-#endif
-
-// Rows per workgroup: R for launches with enough rows to fill the chip many
-// times over, 1 for decode-sized ones (which need every workgroup they can get).
+// Rows per workgroup: 2 for launches with enough rows to fill the chip many
+// times over, 1 for decode-sized ones (which need every workgroup they can
+// get). On MI355X, 16384 rows of a 2048-element slice: two rows per workgroup
+// beat one, and four were no faster than two.
 template <typename T, typename W>
 hipError_t run_shard_apply(const RmsShardArgs& a, hipStream_t stream) {
-  if (AKO_TP_APPLY_ROWS >= 4 && a.rows >= 4096) return run_shard_apply_r<T, W, 4>(a, stream);
-  if (AKO_TP_APPLY_ROWS >= 2 && a.rows >= 4096) return run_shard_apply_r<T, W, 2>(a, stream);
+  if (a.rows >= 4096) return run_shard_apply_r<T, W, 2>(a, stream);
   return run_shard_apply_r<T, W, 1>(a, stream);
 }
 

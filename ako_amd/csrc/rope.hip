@@ -275,7 +275,8 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
 // streams), so the default is one group; ako_set_tuning(1, 2, n) overrides.
 template <typename T, typename TT, bool NEOX>
 hipError_t run_iters(const RopeDev& d, int64_t per_unit, hipStream_t stream) {
-  const int iters = g_rope_tuning.iters > 0 ? g_rope_tuning.iters : 1;
+  const int forced_iters = g_rope_tuning.iters;
+  const int iters = forced_iters > 0 ? forced_iters : 1;
   // Wavefronts per workgroup: one for launches of at most 2048 wavefronts
   // (decode), so that they spread over as many CUs as possible (graph-replayed
   // on MI355X, q of (64, 1, 32, 128): 2.10 us against 2.23 us with four);

@@ -10,12 +10,31 @@ do not share x), 11 GB per step against a 256 MB Infinity Cache, so every
 launch reads cold data. ``value`` is algorithmic bytes per step x steps /
 elapsed device time, in GB/s.
 
-Also reported on the same line:
+The printed line (one JSON object, kept under 8 KB) also carries:
   roofline      the dominant kernel (the slowest launch of the step) with its
                 per-launch duration from HIP events on the launch stream, and
                 a plain device copy of the same byte count timed the same way
                 (copy_same_bytes: what the plainest stream of those bytes
                 reaches; a reference, which a kernel can pass);
+  cpu_baseline  the reference's unfused PyTorch path on host CPU tensors with
+                all of torch's threads: RMSNorm on the step's own 12 cells at
+                full size (the lead figure), RoPE q+k at (4, 2048) and SwiGLU
+                at M = 4096, each the median of its passes with the slowest
+                and fastest; the numpy oracle on one thread beside the RMSNorm
+                figure, on a 64-row sample;
+  selection     the reference's selection (gate + timing + cache record) run
+                here over the configs[1]-[3] grid, decode cells included: how
+                many cells the HIP candidate won, and its largest ulp error
+                per op;
+  decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
+                128 greedy steps, eager PyTorch vs the dispatcher, each also
+                with decode steps replayed from a HIP graph;
+  rope_prefill  RoPE at (4, 2048) as the fused q+k launch, the way the
+                decoder runs it;
+  prefill_floor per op, the prefill cell with the lowest share of peak.
+
+Every timed cell goes to ``--cells-out`` (reports/mi355x/bench_cells.json by
+default) in the reference's report layout, with the selection's rows:
   per_kernel    every launch of the step, each beside its copy ceiling, by
                 per-launch events (as the roofline) and, under back_to_back,
                 on its own as 60 launches between one event pair over cold
@@ -24,25 +43,13 @@ Also reported on the same line:
                 decode-size RMSNorm cells, the KV-cache RoPE and the
                 tensor-parallel RMSNorm halves; streaming cells beside their
                 copy ceiling, decode cells as graph-replayed device time with
-                inputs hot (graph_us) and in no cache (graph_cold_us);
-  rope_prefill  RoPE at (4, 2048) as the fused q+k launch, the way the
-                decoder runs it;
-  selection     the reference's selection (gate + timing + cache record) run
-                here over the configs[1]-[3] grid, decode cells included: how
-                many cells the HIP candidate won;
-  decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
-                128 greedy steps, eager PyTorch vs the dispatcher, each also
-                with decode steps replayed from a HIP graph;
-  cpu_baseline  the reference's unfused PyTorch path (rmsnorm_ref /
-                rmsnorm_residual_ref, restated) on host CPU tensors with all
-                of torch's threads, on the same 12 cells with a bounded row
-                sample; the numpy oracle on one thread beside it.
+                inputs hot (graph_us) and in no cache (graph_cold_us).
 
 ``dtype`` is the arithmetic type of the kernels (fp32); the stored tensors
 are fp16 and bf16 (``config.storage_dtypes``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
-       [--no-selection] [--no-decoder] [--no-cpu]
+       [--no-selection] [--no-decoder] [--no-cpu] [--cells-out PATH]
 """
 
 from __future__ import annotations
@@ -50,6 +57,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import tempfile
 import time
@@ -73,7 +81,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-selection", action="store_true", help="skip the selection over the grid")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decoder", action="store_true", help="skip the configs[4] decoder run")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
+                    help="host time the CPU baseline may take, over all its figures")
+    ap.add_argument("--cells-out", type=Path, default=ROOT / "reports" / "mi355x" / "bench_cells.json",
+                    help="where every timed cell and the selection rows are written (report layout)")
     ap.add_argument("--traffic", type=Path, default=ROOT / "profiles" / "hbm_traffic_hot_path_cells.md",
                     help="rocprofv3 FETCH/WRITE summary (ako_amd.benchmark.rocprof) for the kernels")
     return ap.parse_args()
@@ -324,17 +335,51 @@ def selection(torch):
     with tempfile.TemporaryDirectory(prefix="ako-selection-") as tmp:
         summary = run(Path(tmp), {"rmsnorm", "rmsnorm_residual", "rope", "rope_qk", "swiglu"},
                       warmup=5, repeats=20, quiet=True)
+        rows = []
+        for report in sorted(Path(tmp).glob("selection_*.json")):
+            if report.name == "selection_summary.json":
+                continue
+            data = json.loads(report.read_text())
+            rows += [{"operation": data["operation"], **row} for row in data["comparisons"]]
     summary["win_rate"] = summary.pop("hip_win_rate")
     torch.cuda.empty_cache()
-    return summary
+    return summary, rows
+
+
+def _timed_passes(cells, seconds: float, min_passes: int = 3) -> list[float]:
+    """Seconds per pass over ``cells`` (one untimed pass first), passes
+    repeated until ``seconds`` have gone by and at least ``min_passes`` ran."""
+    for fn in cells:
+        fn()
+    times, t_start = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        for fn in cells:
+            fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= seconds and len(times) >= min_passes:
+            return times
+
+
+def _rate(nbytes: int, times: list[float]) -> dict:
+    """Median GB/s over the passes, with the slowest and fastest pass."""
+    rates = sorted(nbytes / t / 1e9 for t in times)
+    return {"value": round(statistics.median(rates), 3), "spread": [round(rates[0], 3), round(rates[-1], 3)],
+            "passes": len(times)}
 
 
 def cpu_baseline(args, torch, rf, value):
-    """The reference's unfused PyTorch path on the host cores (the lead figure),
-    and the numpy oracle on one thread beside it, on a bounded row sample."""
+    """The reference's unfused PyTorch path on the host cores: every op of
+    the metric, on host CPU tensors with all of torch's threads. RMSNorm (the
+    lead figure) on the step's own 12 cells at full size, RoPE q+k at
+    (4, 2048) and SwiGLU at M = 4096, each the median of its timed passes
+    with the slowest and fastest pass; the numpy oracle on one thread beside
+    the RMSNorm figure, on a row sample."""
     import numpy as np
 
     from ako_amd.ops.rmsnorm_ref import rmsnorm_ref, rmsnorm_residual_ref
+    from ako_amd.ops.rope_ref import build_rope_tables, rope_ref
+    from ako_amd.ops.swiglu_ref import swiglu_ref
     from oracle import ops as oracle
 
     def storage(t):
@@ -342,59 +387,73 @@ def cpu_baseline(args, torch, rf, value):
             return t.view(torch.int16).numpy().view(np.uint16)
         return t.numpy()
 
-    def timed_passes(cells, seconds):
-        for _, fn in cells:
-            fn()
-        passes, t0 = 0, time.perf_counter()
-        while True:
-            for _, fn in cells:
-                fn()
-            passes += 1
-            elapsed = time.perf_counter() - t0
-            if elapsed >= seconds and passes >= 3:
-                return passes, elapsed
-
-    torch_rows, port_rows = 512, 64
+    budget = args.cpu_seconds
+    threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
-    torch_cells, port_cells = [], []
+    # One pool of N(0,1) values; each cell's x and residual are windows of it
+    # at different offsets (drawing 2.8e9 fresh values would take longer than
+    # the timing itself).
+    widest = max(RMS_HIDDEN)
+    pool = torch.randn(RMS_ROWS * widest + 2 * widest, generator=g)
+    rms_cells, rms_bytes, port_cells, port_bytes = [], 0, [], 0
+    port_rows = 64
     for dtype in (torch.float16, torch.bfloat16):
         name = "float16" if dtype == torch.float16 else "bfloat16"
-        for h in RMS_HIDDEN:
-            x = torch.randn(torch_rows, h, generator=g).to(dtype)
-            r = torch.randn(torch_rows, h, generator=g).to(dtype)
+        for i, h in enumerate(RMS_HIDDEN):
+            n = RMS_ROWS * h
+            x = pool[i:i + n].view(RMS_ROWS, h).to(dtype)
+            r = pool[widest + i:widest + i + n].view(RMS_ROWS, h).to(dtype)
             w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
-            torch_cells.append((rf.alg_bytes_rmsnorm(torch_rows, h, dtype), lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6)))
-            torch_cells.append((rf.alg_bytes_rmsnorm_residual(torch_rows, h, dtype),
-                                lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)))
+            rms_cells += [lambda x=x, w=w: rmsnorm_ref(x, w, 1e-6),
+                          lambda x=x, r=r, w=w: rmsnorm_residual_ref(x, r, w, 1e-6)]
+            rms_bytes += rf.alg_bytes_rmsnorm(RMS_ROWS, h, dtype) + rf.alg_bytes_rmsnorm_residual(RMS_ROWS, h, dtype)
             xn, rn, wn = storage(x[:port_rows]), storage(r[:port_rows]), storage(w)
-            port_cells.append((rf.alg_bytes_rmsnorm(port_rows, h, dtype),
-                               lambda xn=xn, wn=wn, name=name: oracle.rmsnorm(xn, wn, 1e-6, dtype=name)))
-            port_cells.append((rf.alg_bytes_rmsnorm_residual(port_rows, h, dtype),
-                               lambda xn=xn, rn=rn, wn=wn, name=name:
-                               oracle.rmsnorm_residual(xn, rn, wn, 1e-6, dtype=name)))
-    threads = torch.get_num_threads()
-    t_passes, t_elapsed = timed_passes(torch_cells, args.cpu_seconds)
-    torch_gbps = sum(b for b, _ in torch_cells) * t_passes / t_elapsed / 1e9
-    p_passes, p_elapsed = timed_passes(port_cells, args.cpu_seconds / 2)
-    port_gbps = sum(b for b, _ in port_cells) * p_passes / p_elapsed / 1e9
-    log(f"cpu baseline: PyTorch unfused reference {torch_gbps:.3f} GB/s on {threads} threads; "
-        f"numpy oracle {port_gbps:.3f} GB/s on 1 thread")
+            port_cells += [lambda xn=xn, wn=wn, name=name: oracle.rmsnorm(xn, wn, 1e-6, dtype=name),
+                           lambda xn=xn, rn=rn, wn=wn, name=name:
+                           oracle.rmsnorm_residual(xn, rn, wn, 1e-6, dtype=name)]
+            port_bytes += (rf.alg_bytes_rmsnorm(port_rows, h, dtype)
+                           + rf.alg_bytes_rmsnorm_residual(port_rows, h, dtype))
+    del pool
+    rms = _rate(rms_bytes, _timed_passes(rms_cells, 0.5 * budget))
+    del rms_cells
+
+    # RoPE: q[4,2048,32,128] and k[4,2048,8,128], fp16 and bf16, tables cast
+    # to the storage dtype.
+    rope_cells, rope_bytes = [], 0
+    cos32, sin32 = build_rope_tables(2048, 128)
+    for dtype in (torch.float16, torch.bfloat16):
+        cos, sin = cos32.to(dtype), sin32.to(dtype)
+        q = torch.randn(4, 2048, 32, 128, generator=g).to(dtype)
+        k = torch.randn(4, 2048, 8, 128, generator=g).to(dtype)
+        rope_cells += [lambda q=q, c=cos, s=sin: rope_ref(q, c, s, "neox"),
+                       lambda k=k, c=cos, s=sin: rope_ref(k, c, s, "neox")]
+        rope_bytes += rf.alg_bytes_rope(4, 2048, 40, 128, dtype, dtype)
+    rope = _rate(rope_bytes, _timed_passes(rope_cells, 0.2 * budget))
+    del rope_cells
+
+    gt = torch.randn(4096, 14336, generator=g).to(torch.bfloat16)
+    ut = torch.randn(4096, 14336, generator=g).to(torch.bfloat16)
+    swiglu = _rate(rf.alg_bytes_swiglu(4096, 14336, torch.bfloat16),
+                   _timed_passes([lambda: swiglu_ref(gt, ut)], 0.15 * budget))
+    del gt, ut
+
+    port = _rate(port_bytes, _timed_passes(port_cells, 0.1 * budget))
+    log(f"cpu baseline ({threads} threads): rmsnorm step {rms['value']} GB/s (passes {rms['spread']}), "
+        f"rope q+k {rope['value']}, swiglu {swiglu['value']}; numpy oracle {port['value']} GB/s on 1 thread")
     return {
-        "value": round(torch_gbps, 3),
+        **rms,
         "unit": "GB/s",
         "cores": threads,
+        "os_cpu_count": os.cpu_count(),
         "kind": "port",
-        "sample": (f"the reference's unfused PyTorch path (rmsnorm_ref / rmsnorm_residual_ref, "
-                   f"ako/ops/rmsnorm_ref.py:8-50 restated) on host CPU tensors with torch's "
-                   f"{threads} threads, os.cpu_count()={os.cpu_count()}: the same 12 cells with "
-                   f"{torch_rows} rows instead of {RMS_ROWS}, {t_passes} passes in {t_elapsed:.1f} s"),
-        "gpu_speedup": round(value / torch_gbps, 1) if torch_gbps > 0 else None,
-        "oracle_numpy": {
-            "value": round(port_gbps, 3),
-            "cores": 1,
-            "sample": (f"oracle.ops.rmsnorm / rmsnorm_residual (numpy, one thread), same cells with "
-                       f"{port_rows} rows: {p_passes} passes in {p_elapsed:.1f} s"),
+        "sample": (f"rmsnorm_ref/rmsnorm_residual_ref (ako/ops/rmsnorm_ref.py:8-50 restated) on host "
+                   f"tensors: the step's 12 cells at full size ({RMS_ROWS} rows), median of passes"),
+        "per_op": {
+            "rope_qk": {**rope, "cells": "rope_ref q[4,2048,32,128]+k[4,2048,8,128], fp16 and bf16, full size"},
+            "swiglu": {**swiglu, "cells": "swiglu_ref [4096,14336] bf16, full size"},
         },
+        "gpu_speedup": round(value / rms["value"], 1) if rms["value"] > 0 else None,
+        "oracle_numpy": {**port, "cores": 1, "cells": f"the same 12 cells with {port_rows} rows"},
     }
 
 
@@ -483,9 +542,8 @@ def main() -> int:
             "gbps": copy["gbps"],
             "frac": copy["frac"],
             "kernel_over_copy": round(dominant.gbps() / copy["gbps"], 4),
-            "source": f"ako_amd/_lib/copy_ceiling {copy['bytes_per_buffer']} (plain 16-byte-packet copy "
-                      f"moving {copy['traffic_bytes']} bytes, cold buffers, per-launch events, "
-                      f"{copy['block']}-lane workgroups, {copy.get('store', 'nt')} stores; the fastest copy found)",
+            "source": f"ako_amd/_lib/copy_ceiling {copy['bytes_per_buffer']}: 16-byte-packet copy, cold "
+                      f"buffers, per-launch events, {copy['block']}-lane groups, {copy.get('store', 'nt')} stores",
         }
         log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
             f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")
@@ -504,10 +562,10 @@ def main() -> int:
                         "kernel": "torch add_ on one element, 64 launches per graph, replayed"}
         log(f"extras: {len(extras)} cells timed; graph launch floor {launch_floor['graph_us']} us")
 
-    picked = None
+    picked, comparisons = None, []
     if not args.no_selection:
         t0 = time.perf_counter()
-        picked = selection(torch)
+        picked, comparisons = selection(torch)
         log(f"selection: HIP chosen in {picked['hip_selected']} of {picked['cells']} cells "
             f"({picked['decode_hip_selected']} of {picked['decode_cells']} decode cells) "
             f"in {time.perf_counter() - t0:.0f} s")
@@ -557,7 +615,20 @@ def main() -> int:
         "extras": extras,
         "launch_floor": launch_floor,
     }
-    print(json.dumps(line), flush=True)
+    from ako_amd.benchmark.benchline import cells_report, compact_line, dumps_line
+    from ako_amd.dispatcher.hardware import get_device_info
+
+    info = get_device_info(dev)
+    report = cells_report(line, info.to_dict(), info.device_name, comparisons)
+    args.cells_out.parent.mkdir(parents=True, exist_ok=True)
+    args.cells_out.write_text(json.dumps(report, indent=1))
+    compact = compact_line(line)
+    try:
+        compact["cells_report"] = str(args.cells_out.resolve().relative_to(ROOT))
+    except ValueError:
+        compact["cells_report"] = str(args.cells_out)
+    log(f"{len(report['results'])} cells and {len(comparisons)} selection rows written to {args.cells_out}")
+    print(dumps_line(compact), flush=True)
     return 0
 
 

@@ -203,11 +203,14 @@ int ako_swiglu_fwd(const void* gate, const void* up, void* y,
                    int dtype, void* stream);
 
 /*
- * Launch-shape override for tuning sweeps (no counterpart in the reference,
- * whose Triton autotuner explored num_warps itself). op: 0 = rmsnorm and
- * rmsnorm_residual, 1 = rope, 2 = swiglu. key/value pairs are documented in
- * the kernel sources; value 0 restores the built-in heuristic. Process-wide,
- * not thread-safe against concurrent launches.
+ * Launch-shape override for tuning sweeps and tests (no counterpart in the
+ * reference, whose Triton autotuner explored num_warps itself); production
+ * callers leave it alone. op: 0 = rmsnorm and rmsnorm_residual, 1 = rope,
+ * 2 = swiglu. key/value pairs are documented in the kernel sources; value 0
+ * restores the built-in heuristic. Process-wide. Each key is an atomic int,
+ * so the call is safe from any host thread: a launch that runs concurrently
+ * sees each key's value from before or after the call (a launch concurrent
+ * with several calls may mix their values).
  */
 int ako_set_tuning(int op, int key, int value);
 

@@ -7,7 +7,13 @@ dispatcher (the HIP candidates win there), ``backend="torch"`` runs the
 reference's unfused eager path (``ako/models/decoder.py:101-216``). GEMMs and
 attention are PyTorch-ROCm in both.
 
-* The truth is a third copy: the torch backend in fp32 with the same
+* A third copy, ``hip``, is the ako backend with every dispatched op forced
+  to its HIP candidate (the reference decoder's per-op ``KernelOverride``,
+  ``ako/models/decoder.py:101-134``): the numerical checks below run on it as
+  on the selected ``ako`` copy, so they hold for the HIP kernels whatever the
+  selector picks, and the selector's decisions are recorded to show which
+  candidate each dispatched call ran.
+* The truth is a fourth copy: the torch backend in fp32 with the same
   (fp16-rounded) weights. The single-op gate (``atol + rtol(fp16)*max|ref|``,
   about one fp16 ulp of the largest logit) is the bar for one kernel's output;
   four layers of fp16 GEMMs and the reference's own ``F.silu(g) * up`` (two
@@ -44,6 +50,10 @@ pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(),
 
 DEV = "cuda"
 PROMPT, STEPS = 512, 128
+#: Every dispatched op of the decoder forced to its HIP candidate.
+FORCE_HIP = {"rmsnorm": "rmsnorm_hip", "rmsnorm_residual": "rmsnorm_residual_hip",
+             "rope_qk": "rope_qk_hip", "swiglu": "swiglu_hip"}
+DISPATCHED = set(FORCE_HIP)
 
 
 @pytest.fixture(scope="module")
@@ -54,6 +64,8 @@ def models():
     cfg.max_seq_len = PROMPT + STEPS
     built = {b: dec.build_lm(cfg, backend=b, device=DEV, dtype=torch.float16, seed=0)
              for b in ("torch", "ako")}
+    built["hip"] = dec.build_lm(cfg, backend="ako", device=DEV, dtype=torch.float16, seed=0,
+                                kernel_override=FORCE_HIP)
     built["fp32"] = copy.deepcopy(built["torch"]).float()
     prompt = torch.randint(0, cfg.vocab_size, (1, PROMPT), generator=torch.Generator().manual_seed(0)).to(DEV)
     yield cfg, built, prompt
@@ -61,13 +73,34 @@ def models():
     torch.cuda.empty_cache()
 
 
-def _errors(logits: dict[str, torch.Tensor]) -> tuple[float, float, float]:
+def _errors(logits: dict[str, torch.Tensor], which: str = "ako") -> tuple[float, float, float]:
     """(dispatched error, native fp16 error) against the fp32 run, and the
-    fp16 gate budget of the fp32 logits."""
+    fp16 gate budget of the fp32 logits; ``which`` names the dispatched copy."""
     ref = logits["fp32"].float()
-    err_a = (logits["ako"].float() - ref).abs().max().item()
+    err_a = (logits[which].float() - ref).abs().max().item()
     err_t = (logits["torch"].float() - ref).abs().max().item()
     return err_a, err_t, error_budget(ref.half())
+
+
+@pytest.fixture
+def decisions(monkeypatch):
+    """Every selection made while the test runs: ``(op, kernel, backend,
+    source)``, with the selector's per-call memo emptied first so that each
+    call site's first call is seen."""
+    from ako_amd.dispatcher import selector as sel
+
+    sel.reset_selector()
+    seen: list[tuple[str, str, str, str]] = []
+    original = sel.KernelSelector.select_entry
+
+    def recording(self, op_name, *args, **kwargs):
+        result = original(self, op_name, *args, **kwargs)
+        seen.append((op_name, result.entry.kernel_name, result.entry.backend, result.source))
+        return result
+
+    monkeypatch.setattr(sel.KernelSelector, "select_entry", recording)
+    yield seen
+    sel.reset_selector()
 
 
 def test_config5_geometry(models) -> None:
@@ -77,41 +110,71 @@ def test_config5_geometry(models) -> None:
     p = next(built["ako"].parameters())
     assert p.dtype == torch.float16 and p.is_cuda
     # Same seed, same weights in every copy.
-    for (na, a), (nt, t), (nf, f) in zip(built["ako"].named_parameters(), built["torch"].named_parameters(),
-                                         built["fp32"].named_parameters()):
-        assert na == nt == nf and torch.equal(a, t) and torch.equal(a.float(), f), na
+    for (na, a), (nt, t), (nh, h), (nf, f) in zip(
+            built["ako"].named_parameters(), built["torch"].named_parameters(),
+            built["hip"].named_parameters(), built["fp32"].named_parameters()):
+        assert na == nt == nh == nf and torch.equal(a, t) and torch.equal(a, h) and torch.equal(a.float(), f), na
 
 
-def test_config5_prefill_and_teacher_forced_decode(models) -> None:
+def test_config5_prefill_and_teacher_forced_decode(models, decisions, monkeypatch) -> None:
     _, built, prompt = models
+    # The selected copy rotates q/k with rope_qk_cache on its preallocated
+    # cache: a direct call of the HIP entry point, not a dispatched op.
+    fused_calls = []
+    direct = dec.rope_qk_cache
+
+    def counting(*args, **kwargs):
+        fused_calls.append(args[0].shape[1])
+        return direct(*args, **kwargs)
+
+    monkeypatch.setattr(dec, "rope_qk_cache", counting)
     caches = {b: m.stack.new_kv_cache(PROMPT + STEPS) for b, m in built.items()}
+    dispatched = ("ako", "hip")
     with torch.no_grad():
         logits = {b: built[b].logits_last(prompt, caches[b]) for b in built}
-        err_a, err_t, budget = _errors(logits)
-        print(f"config5 prefill vs fp32: ako {err_a:.3e}, torch fp16 {err_t:.3e}, gate budget {budget:.3e}",
-              flush=True)
-        assert err_a <= max(2 * err_t, budget), (err_a, err_t, budget)
-        worst, checked, agreed = 0.0, 0, 0
+        for which in dispatched:
+            err_a, err_t, budget = _errors(logits, which)
+            print(f"config5 prefill vs fp32: {which} {err_a:.3e}, torch fp16 {err_t:.3e}, "
+                  f"gate budget {budget:.3e}", flush=True)
+            assert err_a <= max(2 * err_t, budget), (which, err_a, err_t, budget)
+        worst = dict.fromkeys(dispatched, 0.0)
+        checked = dict.fromkeys(dispatched, 0)
+        agreed = dict.fromkeys(dispatched, 0)
         for step in range(STEPS):
-            err_a, err_t, budget = _errors(logits)
-            bar = max(2 * err_t, budget)
-            worst = max(worst, err_a / bar)
-            assert err_a <= bar, f"step {step}: ako {err_a:.3e} > max(2 x torch {err_t:.3e}, {budget:.3e})"
             top2 = logits["fp32"].topk(2, dim=-1).values[0]
             margin = (top2[0] - top2[1]).item()
             truth = logits["fp32"].argmax(-1)
-            a_tok = logits["ako"].argmax(-1)
-            if margin > 2 * err_a:
-                checked += 1
-                assert torch.equal(a_tok, truth), f"step {step}: margin {margin:.3e}, ako token differs"
-            agreed += int(torch.equal(a_tok, truth))
+            for which in dispatched:
+                err_a, err_t, budget = _errors(logits, which)
+                bar = max(2 * err_t, budget)
+                worst[which] = max(worst[which], err_a / bar)
+                assert err_a <= bar, (f"step {step}: {which} {err_a:.3e} > max(2 x torch {err_t:.3e}, "
+                                      f"{budget:.3e})")
+                a_tok = logits[which].argmax(-1)
+                if margin > 2 * err_a:
+                    checked[which] += 1
+                    assert torch.equal(a_tok, truth), f"step {step}: margin {margin:.3e}, {which} token differs"
+                agreed[which] += int(torch.equal(a_tok, truth))
             if step + 1 == STEPS:
                 break
             nxt = truth.view(1, 1)  # teacher forcing: every copy sees the fp32 token
             logits = {b: built[b].logits_last(nxt, caches[b]) for b in built}
-    print(f"config5 decode: {STEPS} steps, worst error / bar {worst:.3f}, argmax checked on {checked}, "
-          f"equal on {agreed}", flush=True)
-    assert checked >= STEPS // 2  # the margin rule must leave most steps checked
+    for which in dispatched:
+        print(f"config5 decode ({which}): {STEPS} steps, worst error / bar {worst[which]:.3f}, argmax checked "
+              f"on {checked[which]}, equal on {agreed[which]}", flush=True)
+        assert checked[which] >= STEPS // 2  # the margin rule must leave most steps checked
+    # What ran: the forced copy's calls are all the HIP entries; the selected
+    # copy's decisions are printed, and HIP must hold at least 90% of them.
+    forced = [d for d in decisions if d[3] == "forced"]
+    chosen = [d for d in decisions if d[3] != "forced"]
+    assert {d[0] for d in forced} == DISPATCHED, forced
+    assert all(d[1] == FORCE_HIP[d[0]] and d[2] == "hip" for d in forced), forced
+    assert {d[0] for d in chosen} == DISPATCHED - {"rope_qk"}, chosen
+    assert len(fused_calls) == 4 * STEPS and fused_calls[0] == PROMPT, fused_calls[:8]
+    hip = sum(d[2] == "hip" for d in chosen)
+    print(f"config5 selected copy: {hip} of {len(chosen)} decisions chose HIP; others: "
+          f"{sorted({d for d in chosen if d[2] != 'hip'})}", flush=True)
+    assert hip >= 0.9 * len(chosen), chosen
 
 
 def test_config5_graphed_decode_matches_eager(models) -> None:
@@ -130,9 +193,11 @@ def test_config5_graphed_decode_matches_eager(models) -> None:
     assert torch.equal(graphed, eager_tokens)
 
 
-def test_config5_layer0_kernels_against_the_oracle(models, monkeypatch) -> None:
+@pytest.mark.parametrize("which", ["hip", "ako"])
+def test_config5_layer0_kernels_against_the_oracle(models, monkeypatch, which) -> None:
     """The dispatched calls of layer 0 at prefill, recorded as the model runs,
-    against the oracle on 64 sampled token rows (rows are independent)."""
+    against the oracle on 64 sampled token rows (rows are independent): on
+    the copy forced to the HIP candidates and on the selected copy."""
     _, built, prompt = models
     seen: dict[str, tuple] = {}
 
@@ -147,7 +212,7 @@ def test_config5_layer0_kernels_against_the_oracle(models, monkeypatch) -> None:
         monkeypatch.setattr(dec, name, record(name, getattr(dec, name)))
     with torch.no_grad():
         # A growing cache (no slab): prefill rotates q and k with rope_qk.
-        built["ako"].logits_last(prompt, built["ako"].stack.new_kv_cache())
+        built[which].logits_last(prompt, built[which].stack.new_kv_cache())
     torch.cuda.synchronize()
     assert set(seen) == {"rmsnorm", "rmsnorm_residual", "rope_qk", "swiglu"}, set(seen)
     rows = np.unique(np.concatenate([[0, PROMPT - 1],
