@@ -81,8 +81,10 @@ def decoder_summary(dec: dict[str, Any] | None) -> dict[str, Any] | None:
             out[k] = dec[k]
     step = dec.get("ako", {}).get("graphed_step_breakdown") or {}
     if step.get("recorded"):
-        out["graphed_step_device_us"] = step["device_us_per_step"]
-        out["graphed_step_library_us"] = step["library_us_per_step"]
+        # Recorded kernel durations under the profiler: each includes the
+        # launch's dispatch behind the kernel before it.
+        out["graphed_step_device_recorded_us"] = step["device_us_per_step"]
+        out["graphed_step_library_recorded_us"] = step["library_us_per_step"]
     return out
 
 
@@ -93,6 +95,9 @@ def compact_line(full: dict[str, Any]) -> dict[str, Any]:
             if k not in ("per_kernel", "extras", "selection", "decoder", "gpu_state")}
     line["selection"] = selection_summary(full.get("selection"))
     line["decoder"] = decoder_summary(full.get("decoder"))
+    in_model = full.get("decode_in_model")
+    if line["decoder"] is not None and in_model:
+        line["decoder"]["library_in_model_us_per_step"] = in_model["step_library_us"]
     rows = list(full.get("per_kernel") or []) + list(full.get("extras") or [])
     line["prefill_floor"] = prefill_floor(rows) or None
     state = full.get("gpu_state") or {}

@@ -213,12 +213,21 @@ def grid_markdown(groups: list[dict[str, Any]], command: str, title: str, note: 
 
 
 def tail_breakdown(rows: list[tuple[str, int, int]], steps: int, *, tail_ms: float | None = None,
-                   marker: str | None = None) -> dict[str, Any]:
+                   marker: str | None = None, library: str = "_ZN3ako") -> dict[str, Any]:
     """Kernel time per step over the last ``steps`` steps of a trace (e.g. the
     replayed decode steps that end a run). The window is either the last
     ``tail_ms`` of the trace, or -- exact -- from the end of the ``steps + 1``-th
     last launch of a kernel whose name contains ``marker`` (one launch per
-    step, such as the argmax) to the end of the last one."""
+    step, such as the argmax) to the end of the last one.
+
+    Two attributions per kernel: ``us_per_step``, the sum of its recorded
+    durations, and ``timeline_us_per_step``, the part of the step's span that
+    ends with it: its end minus the latest end before it. On one stream the
+    second partitions the span exactly, launch gaps included, while recorded
+    durations of short kernels that follow a long one can start before that
+    one has ended (``start_gap_us``, the median of start minus the previous
+    end, is then negative) and count that overlap twice. ``library`` marks
+    this library's kernels for the two totals."""
     if marker is not None:
         marks = [r for r in rows if marker in r[0]]
         if len(marks) < steps + 1:
@@ -228,27 +237,56 @@ def tail_breakdown(rows: list[tuple[str, int, int]], steps: int, *, tail_ms: flo
     elif tail_ms is not None:
         end = rows[-1][2]
         window = [r for r in rows if r[1] >= end - tail_ms * 1e6]
+        begin = window[0][1]
     else:
         raise ValueError("give tail_ms or marker")
     per: dict[str, list[int]] = {}
+    line: dict[str, int] = {}
+    gaps: dict[str, list[int]] = {}
+    last_end = begin
     for name, t0, t1 in window:
         per.setdefault(name, []).append(t1 - t0)
-    span_ns = end - (begin if marker is not None else window[0][1])
-    kernels = sorted(({"name": n, "calls_per_step": len(d) / steps, "us_per_step": sum(d) / steps / 1e3}
-                      for n, d in per.items()), key=lambda k: -k["us_per_step"])
+        line[name] = line.get(name, 0) + max(0, t1 - last_end)
+        gaps.setdefault(name, []).append(t0 - last_end)
+        last_end = max(last_end, t1)
+    span_ns = end - begin
+    kernels = sorted(({"name": n, "calls_per_step": len(d) / steps, "us_per_step": sum(d) / steps / 1e3,
+                       "timeline_us_per_step": line[n] / steps / 1e3,
+                       "start_gap_us": statistics.median(gaps[n]) / 1e3}
+                      for n, d in per.items()), key=lambda k: -k["timeline_us_per_step"])
+    ours = [k for k in kernels if library and library in k["name"]]
     return {"steps": steps, "span_us_per_step": span_ns / steps / 1e3,
-            "busy_us_per_step": sum(k["us_per_step"] for k in kernels), "kernels": kernels}
+            "busy_us_per_step": sum(k["us_per_step"] for k in kernels),
+            "library_us_per_step": sum(k["us_per_step"] for k in ours),
+            "library_timeline_us_per_step": sum(k["timeline_us_per_step"] for k in ours),
+            "library_calls_per_step": sum(k["calls_per_step"] for k in ours),
+            "kernels": kernels}
 
 
-def breakdown_markdown(result: dict[str, Any], command: str, title: str, top: int = 25) -> str:
-    lines = [f"# {title}", "", "Command:", "", "```", command, "```", "",
+def breakdown_markdown(result: dict[str, Any], command: str, title: str, top: int = 25, note: str = "") -> str:
+    lines = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
+    if note:
+        lines += [note, ""]
+    lines += [
              f"Last {result['steps']} steps of the trace: {result['span_us_per_step']:.1f} us per step, "
-             f"{result['busy_us_per_step']:.1f} us of it in kernels.", "",
-             "| kernel | calls / step | us / step | share |", "|---|---:|---:|---:|"]
+             f"{result['busy_us_per_step']:.1f} us of recorded kernel durations.", ""]
+    if "library_timeline_us_per_step" in result:
+        lines += [f"This library: {result['library_calls_per_step']:.1f} launches per step, "
+                  f"{result['library_us_per_step']:.1f} us of recorded durations, "
+                  f"{result['library_timeline_us_per_step']:.1f} us of the step's timeline.", "",
+                  "Timeline: the kernel's end minus the latest end before it (the span is their sum, "
+                  "launch gaps included). Start gap: median of its start minus that previous end; "
+                  "negative when the recorded start falls inside the previous kernel.", ""]
+    lines += ["| kernel | calls / step | duration us / step | timeline us / step | start gap us | share |",
+              "|---|---:|---:|---:|---:|---:|"]
     for k in result["kernels"][:top]:
         name = k["name"] if len(k["name"]) <= 110 else k["name"][:107] + "..."
-        share = 100.0 * k["us_per_step"] / result["span_us_per_step"]
-        lines.append(f"| `{name}` | {k['calls_per_step']:.1f} | {k['us_per_step']:.1f} | {share:.1f}% |")
+        tl = k.get("timeline_us_per_step", k["us_per_step"])
+        share = 100.0 * tl / result["span_us_per_step"]
+        gap = k.get("start_gap_us")
+        gap_s = f"{gap:.2f}" if gap is not None else ""
+        lines.append(f"| `{name}` | {k['calls_per_step']:.1f} | {k['us_per_step']:.1f} | {tl:.1f} | {gap_s} | "
+                     f"{share:.1f}% |")
     return "\n".join(lines) + "\n"
 
 
@@ -336,7 +374,7 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--stats", type=Path, help="a *_kernel_stats.csv to summarise instead")
     ap.add_argument("--trace", type=Path, help="a *_kernel_trace.csv: per-step breakdown of its tail")
     ap.add_argument("--pmc", type=Path, help="a *_counter_collection.csv: every counter per cell (with --manifest)")
-    ap.add_argument("--note", default="", help="with --pmc or --by-grid: a sentence placed above the table")
+    ap.add_argument("--note", default="", help="with --pmc, --by-grid or --trace: a sentence placed above the table")
     ap.add_argument("--by-grid", action="store_true",
                     help="with --trace: durations per (kernel, workgroup, grid) instead of a tail breakdown")
     ap.add_argument("--skip", type=int, default=0, help="with --by-grid: warm-up launches dropped per group")
@@ -371,7 +409,7 @@ def main(argv: list[str] | None = None) -> int:
     elif args.trace and not args.stats:
         result = tail_breakdown(read_kernel_trace(args.trace), args.steps, tail_ms=args.tail_ms,
                                 marker=args.marker)
-        args.md.write_text(breakdown_markdown(result, args.command, args.title))
+        args.md.write_text(breakdown_markdown(result, args.command, args.title, note=args.note))
         record = {"kind": "trace_tail_breakdown", "title": args.title, **result}
     elif args.stats:
         rows = read_kernel_stats(args.stats)

@@ -372,3 +372,30 @@ def time_graph_cold(fns: Sequence[Callable[[], Any]], *, evict_bytes: int | None
         diffs.append((t_both - t_evict) * 1e3 / len(calls))
     del with_calls, alone, scratch
     return statistics.median(diffs)
+
+
+def time_graph_after_producer(pairs: Sequence[tuple[Callable[[], Any], Callable[[], Any]]], *,
+                              replays: int = 4, rounds: int = 5) -> float:
+    """Device microseconds one call adds to a graph in which it runs the way a
+    model runs it: right behind the kernel that writes its input.
+
+    ``pairs`` are ``(producer, call)``: the producer (e.g. the projection GEMV
+    whose output row the call normalises) writes the buffer the call reads,
+    and every pair has buffers of its own, enough of them that one pass over
+    the pairs streams far more than the caches hold. One HIP graph holds
+    ``producer, call`` for every pair, a second the producers alone; the cost
+    per call is the difference of their replay times over the number of
+    pairs: the median over ``rounds`` alternating measurements. It includes
+    what the call's launch costs behind a dependent kernel and its reads of
+    a row another kernel has just written, which a graph of the call alone
+    does not show."""
+    pairs = list(pairs)
+    both = _capture([fn for pair in pairs for fn in pair])
+    alone = _capture([producer for producer, _ in pairs])
+    diffs = []
+    for _ in range(rounds):
+        t_both = _time_replays(both, replays)
+        t_alone = _time_replays(alone, replays)
+        diffs.append((t_both - t_alone) * 1e3 / len(pairs))
+    del both, alone
+    return statistics.median(diffs)

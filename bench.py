@@ -311,6 +311,91 @@ def time_extras(cells, torch, rf, peak, ceilings):
     return extras
 
 
+#: Library calls per graph-replayed configs[4] decode step: an input and a
+#: post-attention residual norm per layer (layer 0's input norm is plain, and
+#: the final norm is a residual one), RoPE with the cache append per layer,
+#: SwiGLU per layer.
+DECODE_STEP_CALLS = {"rmsnorm": 1, "rmsnorm_residual": 8, "rope_qk_cache": 4, "swiglu": 4}
+
+
+def in_model_decode(torch, rf, dev, rnd):
+    """configs[4]'s decode calls as the model runs them: each right behind
+    the fp16 GEMV that writes its input (graph_in_model_us, from
+    ``time_graph_after_producer``), beside the same call on cold inputs with
+    no producer (graph_cold_us). The producers are the model's own
+    projections at batch 1: o_proj (4096 -> 4096) ahead of the residual
+    norm, the fused qkv projection (4096 -> 12288) ahead of RoPE + cache
+    append, gate and up (4096 -> 11008 each) ahead of SwiGLU; every pair has
+    its own weights, so a pass over the pairs streams 1-3 GB and each call
+    finds its inputs, and its own code, as the model leaves them."""
+    from ako_amd.ops.rmsnorm_hip import rmsnorm_hip, rmsnorm_residual_hip
+    from ako_amd.ops.rope_hip import rope_qk_cache_hip
+    from ako_amd.ops.rope_ref import build_rope_tables
+    from ako_amd.ops.swiglu_hip import swiglu_hip
+
+    dt = torch.float16
+    h, heads, d, ffn, slots = 4096, 32, 128, 11008, 640
+    out = {}
+
+    def gemv(n_out):
+        a = rnd(1, h, dtype=dt)
+        w = rnd(n_out, h, dtype=dt, scale=0.02)
+        y = torch.empty(1, n_out, dtype=dt, device=dev)
+        return a, w, y
+
+    def run(name, pairs):
+        calls = [c for _, c in pairs]
+        in_model = rf.time_graph_after_producer(pairs)
+        cold = rf.time_graph_cold(calls)
+        out[name] = {"graph_in_model_us": round(in_model, 3), "graph_cold_us": round(cold, 3),
+                     "per_step": DECODE_STEP_CALLS[name]}
+
+    sets = []
+    for _ in range(32):
+        a, w, x = gemv(h)
+        sets.append((lambda a=a, w=w, x=x: torch.mm(a, w.t(), out=x), x, rnd(1, h, dtype=dt),
+                     rnd(h, dtype=dt, scale=0.1, shift=1.0)))
+    run("rmsnorm_residual", [(p, lambda x=x, r=r, nw=nw: rmsnorm_residual_hip(x, r, nw, 1e-6))
+                             for p, x, r, nw in sets])
+    run("rmsnorm", [(p, lambda x=x, nw=nw: rmsnorm_hip(x, nw, 1e-6)) for p, x, _, nw in sets])
+    del sets
+    torch.cuda.empty_cache()
+
+    cos, sin = build_rope_tables(slots, d, device=dev)
+    pos = torch.full((1,), 511, dtype=torch.long, device=dev)
+    pairs = []
+    for _ in range(16):
+        a, w, qkv = gemv(3 * h)
+        q = qkv[:, :h].view(1, 1, heads, d)
+        k = qkv[:, h:2 * h].view(1, 1, heads, d)
+        v = qkv[:, 2 * h:].view(1, 1, heads, d)
+        kc = torch.zeros(1, heads, slots, d, dtype=dt, device=dev)
+        vc = torch.zeros(1, heads, slots, d, dtype=dt, device=dev)
+        pairs.append((lambda a=a, w=w, y=qkv: torch.mm(a, w.t(), out=y),
+                      lambda q=q, k=k, v=v, kc=kc, vc=vc: rope_qk_cache_hip(q, k, v, cos, sin, pos, kc, vc, "neox")))
+    run("rope_qk_cache", pairs)
+    del pairs
+    torch.cuda.empty_cache()
+
+    pairs = []
+    for _ in range(16):
+        a = rnd(1, h, dtype=dt)
+        wg, wu = rnd(ffn, h, dtype=dt, scale=0.02), rnd(ffn, h, dtype=dt, scale=0.02)
+        g, u = torch.empty(1, ffn, dtype=dt, device=dev), torch.empty(1, ffn, dtype=dt, device=dev)
+
+        def produce(a=a, wg=wg, wu=wu, g=g, u=u):
+            torch.mm(a, wg.t(), out=g)
+            torch.mm(a, wu.t(), out=u)
+        pairs.append((produce, lambda g=g, u=u: swiglu_hip(g, u)))
+    run("swiglu", pairs)
+    del pairs
+    torch.cuda.empty_cache()
+    total = sum(v["graph_in_model_us"] * v["per_step"] for v in out.values())
+    cold = sum(v["graph_cold_us"] * v["per_step"] for v in out.values())
+    return {"ops": out, "step_library_us": round(total, 1), "step_library_cold_us": round(cold, 1),
+            "calls_per_step": sum(DECODE_STEP_CALLS.values())}
+
+
 def rope_prefill_summary(extras, ceilings):
     """RoPE at the prefill shape as the decoder runs it: q and k in one launch."""
     by_name = {r["name"]: r for r in extras}
@@ -548,7 +633,7 @@ def main() -> int:
         log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
             f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")
 
-    extras, launch_floor, rope_prefill = [], None, None
+    extras, launch_floor, rope_prefill, decode_in_model = [], None, None, None
     if not args.no_extras:
         cells = extras_cells(torch, rf, dev, rnd)
         extras = time_extras(cells, torch, rf, peak, ceilings)
@@ -561,6 +646,10 @@ def main() -> int:
         launch_floor = {"graph_us": round(sorted(rf.time_graph_replay(lambda: tiny.add_(1.0)) for _ in range(5))[2], 3),
                         "kernel": "torch add_ on one element, 64 launches per graph, replayed"}
         log(f"extras: {len(extras)} cells timed; graph launch floor {launch_floor['graph_us']} us")
+        decode_in_model = in_model_decode(torch, rf, dev, rnd)
+        log("decode calls behind their producer GEMV (in model) / cold alone, us: " + ", ".join(
+            f"{k} {v['graph_in_model_us']} / {v['graph_cold_us']}" for k, v in decode_in_model["ops"].items())
+            + f"; {decode_in_model['step_library_us']} us per decode step")
 
     picked, comparisons = None, []
     if not args.no_selection:
@@ -611,6 +700,7 @@ def main() -> int:
         "selection": picked,
         "decoder": decoder,
         "rope_prefill": rope_prefill,
+        "decode_in_model": decode_in_model,
         "per_kernel": per_kernel,
         "extras": extras,
         "launch_floor": launch_floor,

@@ -35,6 +35,10 @@ def _full() -> dict:
         "gpu_speedup": 540.0,
         "oracle_numpy": {**rate, "cores": 1, "cells": "64 rows"},
     }
+    full["decode_in_model"] = {
+        "ops": {op: {"graph_in_model_us": 2.7, "graph_cold_us": 2.6, "per_step": n}
+                for op, n in (("rmsnorm", 1), ("rmsnorm_residual", 8), ("rope_qk_cache", 4), ("swiglu", 4))},
+        "step_library_us": 45.0, "step_library_cold_us": 44.0, "calls_per_step": 17}
     full["selection"]["max_err_ulps"] = {"rmsnorm": 0.5, "rmsnorm_residual": 0.5, "rope": 0.0,
                                          "rope_qk": 0.0, "swiglu": 0.06}
     full["selection"]["not_hip"] = [{"cell": f"c{i}", "selected": "rmsnorm_torch_native",
@@ -68,6 +72,8 @@ def test_line_is_strict_json_under_the_limit() -> None:
     dec = line["decoder"]
     assert all(not isinstance(v, (dict, list)) for v in dec.values())  # one level
     assert dec["ako_prefill_ms"] == FULL["decoder"]["ako"]["prefill_ms"]
+    assert dec["library_in_model_us_per_step"] == 45.0
+    assert line["decode_in_model"]["ops"]["swiglu"]["per_step"] == 4
 
 
 def test_line_rejects_non_finite_and_oversize() -> None:

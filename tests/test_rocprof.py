@@ -93,6 +93,33 @@ def test_kernel_stats_and_trace_tail(tmp_path) -> None:
     assert {k["name"]: k["calls_per_step"] for k in marked["kernels"]} == {"gemv": 1.0, "norm": 1.0}
     with pytest.raises(ValueError, match="need"):
         rocprof.tail_breakdown(rows, 9, marker="norm")
+    # Timeline: the marked window opens at a norm's end, so each gemv takes the
+    # 200 us gap before it plus its 600 us, each norm the 100 us gap plus 100 us.
+    tl = {k["name"]: k for k in marked["kernels"]}
+    assert tl["gemv"]["timeline_us_per_step"] == pytest.approx(800.0)
+    assert tl["norm"]["timeline_us_per_step"] == pytest.approx(200.0)
+    assert tl["norm"]["start_gap_us"] == pytest.approx(100.0)
+    assert sum(k["timeline_us_per_step"] for k in marked["kernels"]) == pytest.approx(marked["span_us_per_step"])
+
+
+def test_tail_breakdown_timeline_with_overlapping_records() -> None:
+    """A short kernel whose recorded start falls inside the long kernel before
+    it: its duration counts the overlap, its timeline share does not, and the
+    timeline still sums to the span."""
+    rows, t = [("mark", 0, 1000)], 1000
+    for _ in range(3):  # gemv 600 us; ako kernel recorded from 50 us before gemv ends, 250 us long
+        rows += [("gemv", t + 100_000, t + 700_000), ("_ZN3ako4norm", t + 650_000, t + 900_000),
+                 ("mark", t + 950_000, t + 1_000_000)]
+        t += 1_000_000
+    out = rocprof.tail_breakdown(rows, 3, marker="mark")
+    by = {k["name"]: k for k in out["kernels"]}
+    assert by["_ZN3ako4norm"]["us_per_step"] == pytest.approx(250.0)
+    assert by["_ZN3ako4norm"]["timeline_us_per_step"] == pytest.approx(200.0)
+    assert by["_ZN3ako4norm"]["start_gap_us"] == pytest.approx(-50.0)
+    assert out["library_timeline_us_per_step"] == pytest.approx(200.0)
+    assert out["library_us_per_step"] == pytest.approx(250.0) and out["library_calls_per_step"] == 1.0
+    assert sum(k["timeline_us_per_step"] for k in out["kernels"]) == pytest.approx(out["span_us_per_step"])
+    assert "200.0 us of the step's timeline" in rocprof.breakdown_markdown(out, "cmd", "t")
 
 
 def test_launch_window_cuts_the_event_timed_launches(tmp_path) -> None:
