@@ -21,13 +21,9 @@ import re
 from pathlib import Path
 from typing import Any
 
-_DRM = Path("/sys/class/drm")
+from ako_amd.dispatcher import amdgpu_sysfs
 
-
-def _gpu_device_dirs(drm: Path = _DRM, marker: str = "pp_dpm_sclk") -> list[Path]:
-    """``cardN/device`` directories of the amdgpu cards that expose ``marker``."""
-    cards = sorted(p for p in drm.glob("card[0-9]*") if re.fullmatch(r"card\d+", p.name))
-    return [c / "device" for c in cards if (c / "device" / marker).exists()]
+_DRM = amdgpu_sysfs.DRM
 
 
 def _read(path: Path) -> str | None:
@@ -59,12 +55,12 @@ def _hwmon_value(dev: Path, names: tuple[str, ...], scale: float) -> float | Non
     return None
 
 
-def sample_env(index: int = 0) -> dict[str, Any]:
-    """Clock (MHz), temperature (C) and power (W) of GPU ``index``, or ``None``s."""
-    devices = _gpu_device_dirs()
-    if index >= len(devices):
+def sample_env(index: int = 0, *, drm: Path = _DRM, slot: str | None = None) -> dict[str, Any]:
+    """Clock (MHz), temperature (C) and power (W) of torch's GPU ``index`` (the
+    card at its PCI address, ``amdgpu_sysfs.device_dir``), or ``None``s."""
+    dev = amdgpu_sysfs.device_dir(index, drm=drm, marker="pp_dpm_sclk", slot=slot)
+    if dev is None:
         return {"sm_clock_mhz": None, "temp_c": None, "power_w": None, "throttle_reasons": None}
-    dev = devices[index]
     return {
         "sm_clock_mhz": _active_sclk_mhz(dev),
         "temp_c": _hwmon_value(dev, ("temp1_input", "temp2_input"), 1e3),
@@ -87,7 +83,8 @@ def host_cpu() -> dict[str, Any]:
     return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity}
 
 
-_KFD_PROCS = Path("/sys/class/kfd/kfd/proc")
+_KFD_PROCS = amdgpu_sysfs.KFD_PROCS
+_KFD_TOPOLOGY = amdgpu_sysfs.KFD_TOPOLOGY
 #: Utilisation at or above which the card is taken to be busy (the reference's 3%).
 BUSY_PERCENT = 3.0
 
@@ -100,28 +97,32 @@ def _busy_percent(dev: Path) -> float | None:
         return None
 
 
-def gpu_processes(kfd_proc: Path = _KFD_PROCS) -> list[int] | None:
-    """PIDs with a GPU compute context (any GPU), or None when the KFD is not visible."""
-    try:
-        entries = list(kfd_proc.iterdir())
-    except OSError:
-        return None
-    return sorted(int(p.name) for p in entries if p.name.isdigit())
+def gpu_processes(kfd_proc: Path = _KFD_PROCS, gpu_id: int | None = None) -> list[int] | None:
+    """PIDs with a GPU compute context (on the KFD node ``gpu_id`` when
+    given, else on any GPU), or None when the KFD is not visible."""
+    return amdgpu_sysfs.kfd_processes(gpu_id, kfd_proc)
 
 
 def preflight(index: int = 0, *, strict: bool = True, kfd_proc: Path = _KFD_PROCS,
-              drm: Path | None = None) -> dict[str, Any]:
-    """Check that GPU ``index`` is idle before measuring.
+              drm: Path | None = None, topology: Path = _KFD_TOPOLOGY,
+              slot: str | None = None) -> dict[str, Any]:
+    """Check that torch's GPU ``index`` is idle before measuring.
 
-    Returns ``{"checked", "compute_apps", "utilization_gpu"}``; ``checked`` is
-    False when neither source is readable (a sandbox that hides sysfs). With
-    ``strict`` a busy card raises ``RuntimeError`` (the reference's behaviour);
-    otherwise the state is returned with ``"busy": True`` for the caller to
-    record next to its numbers.
+    The card and the KFD node are the ones at the device's PCI address
+    (``slot``, by default torch's); processes are counted on that GPU only
+    when its KFD node is found, else on any GPU. Returns
+    ``{"checked", "compute_apps", "utilization_gpu"}``; ``checked`` is False
+    when neither source is readable (a sandbox that hides sysfs). With
+    ``strict`` a busy card raises ``RuntimeError`` (the reference's
+    behaviour); otherwise the state is returned with ``"busy": True`` for the
+    caller to record next to its numbers.
     """
-    devices = _gpu_device_dirs(drm if drm is not None else _DRM, "gpu_busy_percent")
-    used = _busy_percent(devices[index]) if index < len(devices) else None
-    pids = gpu_processes(kfd_proc)
+    slot = slot if slot is not None else amdgpu_sysfs.torch_pci_slot(index)
+    dev = amdgpu_sysfs.device_dir(index, drm=drm if drm is not None else _DRM, marker="gpu_busy_percent",
+                                  slot=slot)
+    used = _busy_percent(dev) if dev is not None else None
+    gpu_id = amdgpu_sysfs.kfd_gpu_id(slot, topology) if slot is not None else None
+    pids = gpu_processes(kfd_proc, gpu_id)
     mine = os.getpid()
     foreign = [p for p in (pids or []) if p != mine]
     state: dict[str, Any] = {"checked": used is not None or pids is not None,

@@ -172,6 +172,7 @@ int ako_set_tuning(int op, int key, int value) {
     case 1:
       if (key == 1) { ako::g_rope_tuning.tokens_per_block = value; return AKO_OK; }
       if (key == 2) { ako::g_rope_tuning.iters = value; return AKO_OK; }
+      if (key == 3) { ako::g_rope_tuning.xcd_chunk = value; return AKO_OK; }
       break;
     case 2:
       if (key == 1) { ako::g_swiglu_tuning.vecs_per_thread = value; return AKO_OK; }

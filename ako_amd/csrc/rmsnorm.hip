@@ -69,7 +69,7 @@ struct WeightPacket {
 // points of peak, residual fp16 rows +0.8 with one packet per load group
 // (with whole groups, -1.6), residual bf16 unchanged; rows of 8 KiB or less
 // were slower (pipelined 16 KiB-input rows: 82-87% down to 69-70%), so only
-// the (16, 2) shape has the variant.
+// the (16, 2) shape and the bf16 residual rows of the (16, 1) shape use it.
 constexpr int kRawBufferWord3 = 0x00020000;  // raw (untyped) access, gfx9 CDNA layout
 constexpr int kStoreSc1Nt = 18;              // cache policy bits: nt (2) | sc1 (16)
 
@@ -78,36 +78,6 @@ __device__ __forceinline__ void store_write_through(T* row_base, int row_bytes, 
   static_assert(E * sizeof(T) == 16, "whole 16-byte packets");
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(row_base, 0, row_bytes, kRawBufferWord3);
   __builtin_amdgcn_raw_buffer_store_b128(pk.raw, r, elem * static_cast<int>(sizeof(T)), 0, kStoreSc1Nt);
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
-// XCD b % 8). block_order hands each XCD runs of `chunk` consecutive blocks:
-// workgroup b = 8 i + x takes block c * 8 chunk + x * chunk + j for
-// i = c * chunk + j, so the XCDs walk 8 separate runs instead of interleaving
-// block by block. chunk <= 1 is the identity; the last, partial round of runs
-// is split evenly the same way and the n % 8 trailing blocks keep their own
-// index, which keeps the map a bijection on [0, n).
-struct XcdRuns {
-  unsigned chunk;    // consecutive blocks per run; <= 1 keeps block order
-  FastDiv by_chunk;  // divides by max(chunk, 1)
-};
-
-inline XcdRuns make_xcd_runs(unsigned chunk) { return XcdRuns{chunk, make_fastdiv(chunk > 1 ? chunk : 1)}; }
-
-// The two divisions by the run length are multiply-shifts (a runtime
-// division costs a reciprocal-and-correct sequence on the path to a new
-// workgroup's first load). Block order (every decode-sized launch) returns
-// before any of it: computing the runs anyway, without the branch, made
-// one-row launches 0.06-0.2 us slower.
-__device__ __forceinline__ unsigned block_order(unsigned b, unsigned n, const XcdRuns& r) {
-  const unsigned q = n / 8;
-  if (r.chunk <= 1 || b >= 8 * q) return b;
-  const unsigned x = b % 8, i = b / 8;
-  const unsigned full = fast_div(q, r.by_chunk);
-  const unsigned c = fast_div(i, r.by_chunk), j = i - c * r.chunk;
-  if (c < full) return c * 8 * r.chunk + x * r.chunk + j;
-  const unsigned rest = q - full * r.chunk;
-  return full * 8 * r.chunk + x * rest + (i - full * r.chunk);
 }
 
 template <typename T, typename W, int WPR, int VPT, int RPB, bool RES, bool EW, bool SPLIT = false,
@@ -697,10 +667,17 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   // -3.5% fp16).
   // Rows of 8193-16384 elements at 16 wavefronts x 2 packets in launches of
   // many rows store write-through (see store_write_through); residual rows
-  // then take one packet per load group, fp16 and bf16 alike.
-  if constexpr (VPT == 2 && WPR == 16) {
+  // then take one packet per load group, fp16 and bf16 alike. So do bf16
+  // residual rows at 16 wavefronts x 1 packet (4097-8192 elements): medians
+  // of 7 interleaved rotating runs on MI355X, 16384 x 8192, three boxes, +0.7
+  // to +0.9 points of peak (78.0 -> 78.9%); fp16 rows there were -0.5 to +0.2
+  // and keep non-temporal stores. fp32 rows of 8192 on the (16, 2) shape:
+  // plain 80.6% against 78.2% with non-temporal stores, residual 82.5%
+  // against 81.2%.
+  if constexpr ((VPT == 2 || VPT == 1) && WPR == 16) {
+    constexpr bool kWtByDefault = VPT == 2 || (RES && std::is_same_v<T, __bf16>);
     const int wt_forced = g_rms_tuning.write_through;
-    if (wt_forced == 2 || (wt_forced == 0 && a.rows > kFewRows)) {
+    if (wt_forced == 2 || (wt_forced == 0 && kWtByDefault && a.rows > kFewRows)) {
       if constexpr (RES) {
         if (g_rms_tuning.load_groups != 1) return run_reg_launch<T, W, WPR, VPT, RES, false, true, true>(a, stream);
       }

@@ -59,6 +59,7 @@ struct RopeDev {
   int64_t st;
   int64_t total_tokens;  // batch * seq (scalar kernel)
   FastDiv by_chunks, by_seq;  // dividers for chunks and seq (vector kernel)
+  XcdRuns runs;               // workgroup order over the XCDs (vector kernel)
 };
 
 template <typename T, typename TT, bool NEOX, int ITERS, int TPB, bool CACHE>
@@ -76,7 +77,8 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   // argument can be fetched at once at the start instead of one scalar load
   // round trip after another.
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = static_cast<int>(blockIdx.x) * TPB + static_cast<int>(threadIdx.x) / kWave;
+  const int wave = static_cast<int>(block_order(blockIdx.x, gridDim.x, a.runs)) * TPB +
+                   static_cast<int>(threadIdx.x) / kWave;
   const int tl_any = static_cast<int>(fast_div(static_cast<unsigned>(wave), a.by_chunks));
   const bool live = tl_any < a.tokens;
   const int tl = live ? tl_any : 0;
@@ -255,6 +257,8 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
   d.by_chunks = make_fastdiv(static_cast<unsigned>(d.chunks));
   d.by_seq = make_fastdiv(static_cast<unsigned>(d.seq));
   d.pu_shift = (per_unit & (per_unit - 1)) == 0 ? __builtin_ctzll(per_unit) : -1;
+  const int chunk = g_rope_tuning.xcd_chunk;
+  d.runs = make_xcd_runs(chunk > 1 ? static_cast<unsigned>(chunk) : 1u);
   const int64_t tokens_per_launch = std::max<int64_t>(1, kWavesPerLaunch / d.chunks);
   for (int64_t first = 0; first < d.total_tokens; first += tokens_per_launch) {
     RopeDev part = d;

@@ -20,6 +20,12 @@ nor do an MI350X and an MI355X (the same ISA and CU count, 2200 against
 2400 MHz). Some boxes report an empty name instead of the generic one for the
 same part; ``part_label`` maps both to "AMD Radeon Graphics", so the key does
 not change from box to box.
+
+The clock comes from HIP's ``clockRate`` when the library is loaded, else from
+the highest level of the card's ``pp_dpm_sclk`` (the card matched by PCI
+address, ``amdgpu_sysfs``); the two agree (2400 MHz on MI355X). An identity
+still missing its clock is not memoised, so a process that asks before the
+library loads does not keep a key that other processes never use.
 """
 
 from __future__ import annotations
@@ -29,6 +35,8 @@ from functools import lru_cache
 from pathlib import Path
 
 import torch
+
+from ako_amd.dispatcher import amdgpu_sysfs
 
 
 @dataclass(frozen=True)
@@ -156,15 +164,38 @@ def get_device_info(device: torch.device | str | None = None) -> DeviceInfo:
     return _device_info(device.type, index)
 
 
+_INFO_CACHE: dict[tuple[str, int | None], DeviceInfo] = {}
+
+
 def clear_device_cache() -> None:
     """Forget memoised probes (tests)."""
-    _device_info.cache_clear()
+    _INFO_CACHE.clear()
     _compute_backend.cache_clear()
     _amdgpu_module_version.cache_clear()
 
 
-@lru_cache(maxsize=None)
+def sysfs_clock_khz(index: int) -> int | None:
+    """Peak engine clock of torch's GPU ``index`` from the card's
+    ``pp_dpm_sclk``, or None when sysfs does not show it."""
+    dev = amdgpu_sysfs.device_dir(index, marker="pp_dpm_sclk")
+    return amdgpu_sysfs.peak_sclk_khz(dev) if dev is not None else None
+
+
 def _device_info(device_type: str, device_index: int | None) -> DeviceInfo:
+    key = (device_type, device_index)
+    cached = _INFO_CACHE.get(key)
+    if cached is not None:
+        return cached
+    info = _probe_device(device_type, device_index)
+    # A ROCm identity without its clock (no library, no sysfs) is answered
+    # but not kept: a later call, once either source is there, gets the key
+    # that every other process uses.
+    if info.compute_backend != "rocm" or info.clock_mhz is not None:
+        _INFO_CACHE[key] = info
+    return info
+
+
+def _probe_device(device_type: str, device_index: int | None) -> DeviceInfo:
     backend = _compute_backend()
     if device_type == "cuda" and torch.cuda.is_available():
         index = device_index or 0
@@ -174,6 +205,8 @@ def _device_info(device_type: str, device_index: int | None) -> DeviceInfo:
         arch = ident.get("arch") or getattr(props, "gcnArchName", None)
         cus = _int_or_none(ident.get("cus")) or getattr(props, "multi_processor_count", None)
         clock_khz = _int_or_none(ident.get("clock_khz"))
+        if clock_khz is None and backend == "rocm":
+            clock_khz = sysfs_clock_khz(index)
         mem_bytes = _int_or_none(ident.get("mem_bytes")) or props.total_memory
         raw_name = ident.get("name") or props.name
         name = part_label(raw_name, arch, cus, clock_khz, mem_bytes) if backend == "rocm" else props.name

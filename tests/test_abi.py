@@ -193,8 +193,9 @@ def test_tuning_keys(lib) -> None:
     assert lib.ako_set_tuning(0, 10, 33) == INVALID  # pipelined workgroups per CU: at most 32
     assert lib.ako_set_tuning(0, 11, 3) == INVALID  # load groups: 0, 1 or 2
     assert lib.ako_set_tuning(0, 12, 3) == INVALID  # write-through stores: 0, 1 or 2
+    assert lib.ako_set_tuning(1, 4, 0) == INVALID  # RoPE has three keys
     for op, key in ((0, 1), (0, 2), (0, 3), (0, 4), (0, 5), (0, 6), (0, 7), (0, 8), (0, 9), (0, 10), (0, 11), (0, 12), (1, 1),
-                    (1, 2), (2, 1)):
+                    (1, 2), (1, 3), (2, 1)):
         assert lib.ako_set_tuning(op, key, 0) == OK
 
 

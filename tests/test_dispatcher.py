@@ -237,9 +237,20 @@ def test_cache_key_tells_amd_parts_apart(monkeypatch) -> None:
     assert keys["mi355x"] == "AMD_Radeon_Graphics_gfx950_256CU_2400MHz_288GB_0"
     assert keys["mi300x"] == "AMD_Radeon_Graphics_gfx942_304CU_2100MHz_192GB_0"
     assert len(set(keys.values())) == 3
-    # Without the library (torch's properties only): no clock, still the ISA.
+    # Without the library the clock comes from the card's pp_dpm_sclk, and
+    # the key is the one the library gives.
     hardware = _fake_rocm_device(monkeypatch, "mi300x", library=False)
+    monkeypatch.setattr(hardware, "sysfs_clock_khz", lambda i: 2_100_000)
+    assert hardware.get_device_info("cuda:0").cache_key == keys["mi300x"]
+    # With neither source: no clock, still the ISA, and the short key is not
+    # memoised, so the full key appears as soon as a source does.
+    hardware = _fake_rocm_device(monkeypatch, "mi300x", library=False)
+    monkeypatch.setattr(hardware, "sysfs_clock_khz", lambda i: None)
     assert hardware.get_device_info("cuda:0").cache_key == "AMD_Radeon_Graphics_gfx942_304CU_192GB_0"
+    monkeypatch.setattr(hardware, "sysfs_clock_khz", lambda i: 2_100_000)
+    assert hardware.get_device_info("cuda:0").cache_key == keys["mi300x"]
+    monkeypatch.setattr(hardware, "sysfs_clock_khz", lambda i: None)
+    assert hardware.get_device_info("cuda:0").cache_key == keys["mi300x"]  # now memoised
     hardware.clear_device_cache()
 
 
@@ -264,8 +275,8 @@ def test_empty_hip_name_keeps_the_generic_cache_key(monkeypatch) -> None:
     generic = hardware.get_device_info("cuda:0").cache_key
     for library in (True, False):
         hardware = _fake_rocm_device(monkeypatch, "mi355x", library=library, name="")
-        key = hardware.get_device_info("cuda:0").cache_key
-        assert key == (generic if library else "AMD_Radeon_Graphics_gfx950_256CU_288GB_0")
+        monkeypatch.setattr(hardware, "sysfs_clock_khz", lambda i: 2_400_000)
+        assert hardware.get_device_info("cuda:0").cache_key == generic
     hardware.clear_device_cache()
 
 
@@ -289,9 +300,9 @@ def test_reference_test_hooks(tmp_path, monkeypatch) -> None:
     assert rmsnorm_torch._compiled == {}
 
     first = get_device_info("cpu")
-    assert hardware._device_info.cache_info().currsize >= 1
+    assert len(hardware._INFO_CACHE) >= 1
     hardware.clear_device_cache()
-    assert hardware._device_info.cache_info().currsize == 0
+    assert len(hardware._INFO_CACHE) == 0
     assert get_device_info("cpu") == first
 
     path = tmp_path / "baseline.json"

@@ -326,19 +326,22 @@ def test_rmsnorm_residual_load_groups_match(dtype, w_dtype) -> None:
 
 
 # (dtype, weight dtype, hidden, row stride or None): rows on the (16, 2) shape,
-# full (16384 half / 8192 fp32 elements) and with idle lanes (9000, 12000).
+# full (16384 half / 8192 fp32 elements) and with idle lanes (9000, 12000), and
+# residual rows on the (16, 1) shape (8192 half elements; 7000 with idle lanes).
 WRITE_THROUGH_CASES = [
     (torch.float16, torch.float16, 16384, None),
     (torch.bfloat16, torch.float32, 16384, 16448),
     (torch.float16, torch.float16, 12000, None),
     (torch.bfloat16, torch.bfloat16, 9000, 9008),
     (torch.float32, torch.float32, 8192, None),
+    (torch.float16, torch.float16, 8192, None),
+    (torch.bfloat16, torch.bfloat16, 7000, 7008),
 ]
 
 
 @pytest.mark.parametrize("dtype,w_dtype,h,stride", WRITE_THROUGH_CASES)
 def test_rmsnorm_write_through_stores_match(dtype, w_dtype, h, stride) -> None:
-    """Rows on the (16, 2) shape stored write-through (key 12 = 2, buffer
+    """Rows on the (16, 2) and (16, 1) shapes stored write-through (key 12 = 2, buffer
     stores with sc1 nt on a resource covering the row) and with plain
     non-temporal stores (key 12 = 1), residual rows with either load grouping:
     the same values in the same places, so bit-identical outputs, also where
@@ -670,6 +673,30 @@ def test_rope_every_iteration_count() -> None:
             assert_rope_exact(expected, to_np(rope_hip(x, cos, sin)), torch.float16)
     finally:
         _native.set_tuning(1, 2, 0)
+
+
+def test_rope_xcd_runs_cover_every_head() -> None:
+    """RoPE with workgroups handed to the XCDs in runs (key 3): the map is a
+    bijection on the grid, so every run length, including ones that leave a
+    partial last round and trailing blocks, gives the oracle's exact output,
+    for q alone and for q and k in one launch."""
+    from ako_amd import _native
+
+    q = grandn((3, 37, 32, 128), torch.bfloat16, 15)
+    k = grandn((3, 37, 8, 128), torch.bfloat16, 16)
+    cos, sin = build_rope_tables(37, 128, device=DEV)
+    cos, sin = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
+    eq = oracle.rope(to_np(q), to_np(cos), to_np(sin), "neox", dtype="bfloat16", table_dtype="bfloat16")
+    ek = oracle.rope(to_np(k), to_np(cos), to_np(sin), "neox", dtype="bfloat16", table_dtype="bfloat16")
+    try:
+        for chunk in (0, 2, 3, 8, 16, 1000):
+            _native.set_tuning(1, 3, chunk)
+            assert_rope_exact(eq, to_np(rope_hip(q, cos, sin)), torch.bfloat16)
+            qo, ko = rope_qk_hip(q, k, cos, sin)
+            assert_rope_exact(eq, to_np(qo), torch.bfloat16)
+            assert_rope_exact(ek, to_np(ko), torch.bfloat16)
+    finally:
+        _native.set_tuning(1, 3, 0)
 
 
 def test_rope_rejects_bad_input() -> None:

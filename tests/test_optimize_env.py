@@ -95,3 +95,66 @@ def test_environment_report_on_the_cpu(capsys) -> None:
     assert env.main([]) == 0
     out = capsys.readouterr().out
     assert "hip_library" in out and "CPU only" in out
+
+
+def _two_cards(tmp_path):
+    """A DRM tree with card2 and card10 (card10 sorts first as a string), each
+    with its PCI address, clock levels and load, and a KFD tree with a CPU node
+    and both GPU nodes."""
+    drm = tmp_path / "drm"
+    for card, slot, busy, sclk in (("card2", "0000:5a:00.0", "0", "0: 500Mhz *\n1: 2400Mhz\n"),
+                                   ("card10", "0000:c3:00.0", "80", "0: 500Mhz\n1: 2200Mhz *\n")):
+        dev = drm / card / "device"
+        dev.mkdir(parents=True)
+        (dev / "uevent").write_text(f"DRIVER=amdgpu\nPCI_CLASS=12000\nPCI_SLOT_NAME={slot}\n")
+        (dev / "gpu_busy_percent").write_text(busy + "\n")
+        (dev / "pp_dpm_sclk").write_text(sclk)
+    (drm / "card2-DP-1").mkdir()  # connectors are not cards
+    topo = tmp_path / "topology"
+    for node, gpu_id, location in (("0", "0", 0), ("1", "28206", 0x5A00), ("2", "41733", 0xC300)):
+        (topo / node).mkdir(parents=True)
+        (topo / node / "gpu_id").write_text(gpu_id + "\n")
+        (topo / node / "properties").write_text(f"cpu_cores_count 0\nlocation_id {location}\ndomain 0\n")
+    kfd = tmp_path / "kfd_proc"
+    for pid, entries in ((os.getpid(), ["vram_28206", "queues"]), (4242, ["vram_41733", "sdma_41733"]),
+                         (5151, ["queues"])):
+        for e in entries:
+            (kfd / str(pid) / e).mkdir(parents=True)
+    return drm, topo, kfd
+
+
+def test_cards_are_matched_by_pci_address(tmp_path) -> None:
+    """Cards sort by number (card2 before card10); a PCI address picks its
+    card whatever its position; the peak clock is the highest sclk level,
+    not the active one; the KFD node is found by domain and location id."""
+    from ako_amd.dispatcher import amdgpu_sysfs as sysfs
+
+    drm, topo, _ = _two_cards(tmp_path)
+    assert [d.parent.name for d in sysfs.card_device_dirs(drm)] == ["card2", "card10"]
+    assert sysfs.device_dir(1, drm=drm, slot="0000:5A:00.0").parent.name == "card2"
+    assert sysfs.device_dir(0, drm=drm, slot="0000:c3:00.0").parent.name == "card10"
+    assert sysfs.device_dir(0, drm=drm, slot="0000:01:00.0") is None
+    assert sysfs.peak_sclk_khz(drm / "card2" / "device") == 2_400_000
+    assert sysfs.peak_sclk_khz(drm / "card10" / "device") == 2_200_000
+    assert sysfs.pci_slot_name(0, 0x5A, 0) == "0000:5a:00.0"
+    assert sysfs.kfd_gpu_id("0000:5a:00.0", topo) == 28206
+    assert sysfs.kfd_gpu_id("0000:c3:00.0", topo) == 41733
+    assert sysfs.kfd_gpu_id("0000:77:00.0", topo) is None
+    # Without torch's PCI address (no GPU here) the index is the card-number position.
+    assert sysfs.device_dir(1, drm=drm).parent.name == "card10"
+
+
+def test_preflight_looks_at_its_own_card(tmp_path) -> None:
+    """The idle card2 with only this process on it passes even though card10
+    is busy and another process holds a context there; card10 is refused for
+    its load and its process; a process with no per-GPU entries counts on
+    both."""
+    drm, topo, kfd = _two_cards(tmp_path)
+    state = env.preflight(0, drm=drm, kfd_proc=kfd, topology=topo, slot="0000:5a:00.0", strict=False)
+    assert state["utilization_gpu"] == 0.0 and state["compute_apps"] == [5151]
+    state = env.preflight(0, drm=drm, kfd_proc=kfd, topology=topo, slot="0000:c3:00.0", strict=False)
+    assert state["busy"] and state["utilization_gpu"] == 80.0 and state["compute_apps"] == [4242, 5151]
+    # An unknown node: every process counts.
+    assert env.gpu_processes(kfd) == sorted([os.getpid(), 4242, 5151])
+    sample = env.sample_env(0, drm=drm, slot="0000:c3:00.0")
+    assert sample["sm_clock_mhz"] == 2200.0
