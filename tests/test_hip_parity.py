@@ -1103,3 +1103,61 @@ def test_tensors_beyond_2_31_elements() -> None:
     np.testing.assert_array_equal(to_np(y[:, sel]), expected)
     del x, y
     torch.cuda.empty_cache()
+
+
+def _bf16_pairs() -> tuple[np.ndarray, np.ndarray]:
+    """Every bf16 pattern (x) against eight partners (r): two random
+    permutations, itself (doubling: overflow, subnormals doubled), its
+    negation (exact cancellation to +0, -0 + +0), +0, -0, and the smallest
+    positive and negative subnormals (steps across zero and the subnormal
+    range). 524288 pairs."""
+    every = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(91)
+    partners = [rng.permutation(every), rng.permutation(every), every, every ^ np.uint16(0x8000),
+                np.zeros_like(every), np.full_like(every, 0x8000), np.full_like(every, 0x0001),
+                np.full_like(every, 0x8001)]
+    return np.tile(every, len(partners)), np.concatenate(partners)
+
+
+def _assert_same_bits(got: torch.Tensor, ref_bits: np.ndarray, what: str) -> None:
+    """Bit-identical, except that two NaNs match whatever their payloads."""
+    g = got.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    r = ref_bits.reshape(-1)
+
+    def nan(b):
+        return ((b & 0x7F80) == 0x7F80) & ((b & 0x007F) != 0)
+
+    bad = (g != r) & ~(nan(g) & nan(r))
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} differ, first at {int(np.argmax(bad))}: "
+                           f"got {g[bad][:4]}, want {r[bad][:4]}")
+
+
+# (hidden, rows of the 524288 pairs repeated `copies` times): the residual
+# sum through each kernel that adds packets: rmsnorm_reg at (8, 1) with early
+# weights and through rmsnorm_pipe (4096), at (16, 1) with non-temporal and,
+# from 257 rows, write-through stores (8192), at (16, 2) (16384), and
+# rmsnorm_stream for rows past the register budget (131072).
+BF16_SUM_CASES = [(4096, 1), (4096, 3), (8192, 1), (8192, 5), (16384, 1), (16384, 9), (131072, 1)]
+
+
+@pytest.mark.parametrize("hidden,copies", BF16_SUM_CASES, ids=[f"{h}x{c}" for h, c in BF16_SUM_CASES])
+def test_bf16_residual_sum_every_pattern(hidden, copies) -> None:
+    """The rounded residual sum s = bf16(x + r) for every bf16 x against
+    eight partners each (signed zeros, subnormals, overflow to infinity,
+    cancellation, NaN and infinities included), bit for bit against the
+    oracle's fp32 add and round-to-nearest-even, through every kernel that
+    adds 16-byte packets. The tensor-parallel partial half, which adds the
+    same way, is checked on the same pairs."""
+    from ako_amd.ops.rmsnorm_tp import rmsnorm_shard_partial_hip
+
+    xb, rb = _bf16_pairs()
+    with np.errstate(over="ignore", invalid="ignore"):  # overflow to inf and inf - inf are among the cases
+        want = oracle.round_to(oracle.to_f32(xb, "bfloat16") + oracle.to_f32(rb, "bfloat16"), "bfloat16")
+    x = _bits_tensor(xb.reshape(-1, hidden), torch.bfloat16).repeat(copies, 1)
+    r = _bits_tensor(rb.reshape(-1, hidden), torch.bfloat16).repeat(copies, 1)
+    w = torch.ones(hidden, dtype=torch.bfloat16, device=DEV)
+    _, s = rmsnorm_residual_hip(x, r, w)
+    _assert_same_bits(s, np.tile(want.reshape(-1, hidden), (copies, 1)), f"rmsnorm_residual {tuple(x.shape)}")
+    if copies == 1 and hidden <= 8192:
+        s_tp, _ = rmsnorm_shard_partial_hip(x, r)
+        _assert_same_bits(s_tp, want, f"rmsnorm_shard_partial {tuple(x.shape)}")
