@@ -29,8 +29,9 @@ The printed line (one JSON object, kept under 8 KB) also carries:
   decoder       configs[4]: the 4-layer fp16 decoder, prefill 512 tokens then
                 128 greedy steps, eager PyTorch vs the dispatcher, each also
                 with decode steps replayed from a HIP graph;
-  rope_prefill  RoPE at (4, 2048) as the fused q+k launch, the way the
-                decoder runs it;
+  rope_prefill  RoPE at (4, 2048) as the fused q+k launch, and as the
+                decoder's own prefill call, which also writes k and v into
+                its KV cache (qk_cache);
   prefill_floor per op, the prefill cell with the lowest share of peak.
 
 Every timed cell goes to ``--cells-out`` (reports/mi355x/bench_cells.json by
@@ -212,6 +213,21 @@ def extras_cells(torch, rf, dev, rnd):
             add(f"rope_qk_{tag}_{b}x{s}", rf.alg_bytes_rope(b, s, 40, 128, dtype, dtype),
                 lambda i, c=cos, sn=sin, qs=qs, ks=ks: (lambda q=qs[i], k=ks[i]: rope_qk_hip(q, k, c, sn, "neox")),
                 n, decode)
+            if (b, s) == (4, 2048):
+                # The decoder's prefill call: q rotated, k rotated and v copied
+                # into heads-major KV caches at slot 0, one launch per copy,
+                # each copy with caches of its own.
+                nb = rf.alg_bytes_rope_qk_cache(b, s, 32, 8, 128, dtype, dtype)
+                nc = rf.copies_for_cold(nb, dev)
+                vs = [rnd(b, s, 8, 128, dtype=dtype) for _ in range(nc)]
+                caches = [(torch.empty(b, 8, s, 128, dtype=dtype, device=dev),
+                           torch.empty(b, 8, s, 128, dtype=dtype, device=dev)) for _ in range(nc)]
+                pos0 = torch.zeros(1, dtype=torch.long, device=dev)
+                add(f"rope_qk_cache_{tag}_{b}x{s}_q32_kv8", nb,
+                    lambda i, c=cos, sn=sin, qs=qs, ks=ks, vs=vs, caches=caches, p=pos0:
+                        (lambda q=qs[i % len(qs)], k=ks[i % len(ks)], v=vs[i], kv=caches[i]:
+                         rope_qk_cache_hip(q, k, v, c, sn, p, kv[0], kv[1], "neox")),
+                    nc, False)
     # configs[4] decode step, one layer: RoPE of q and k plus the KV-cache
     # append, fused (one launch) and as the unfused sequence it replaces.
     dtype = torch.float16
@@ -397,16 +413,22 @@ def in_model_decode(torch, rf, dev, rnd):
 
 
 def rope_prefill_summary(extras, ceilings):
-    """RoPE at the prefill shape as the decoder runs it: q and k in one launch."""
+    """RoPE at the prefill shape: q and k in one launch (configs[2]'s pair),
+    and the decoder's own call, which also writes k and v into the KV cache."""
     by_name = {r["name"]: r for r in extras}
     out = {}
     for tag in ("fp16", "bf16"):
         qk = by_name.get(f"rope_qk_{tag}_4x2048")
         k = by_name.get(f"rope_k_{tag}_4x2048x8x128")
+        cache = by_name.get(f"rope_qk_cache_{tag}_4x2048_q32_kv8")
         if qk is None:
             continue
         out[tag] = {"cell": qk["name"], "pct_hbm_peak": qk["pct_hbm_peak"],
                     "copy_pct_hbm_peak": qk.get("copy_pct_hbm_peak"), "kernel_over_copy": qk.get("kernel_over_copy")}
+        if cache is not None:
+            out[tag]["qk_cache"] = {"pct_hbm_peak": cache["pct_hbm_peak"],
+                                    "copy_pct_hbm_peak": cache.get("copy_pct_hbm_peak"),
+                                    "kernel_over_copy": cache.get("kernel_over_copy")}
         if k is not None:
             out[tag]["k_alone"] = {"pct_hbm_peak": k["pct_hbm_peak"], "copy_pct_hbm_peak": k.get("copy_pct_hbm_peak"),
                                    "note": "34 MB launch: a copy of that size reaches little more"}
