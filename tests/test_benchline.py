@@ -19,9 +19,12 @@ from ako_amd.benchmark.benchline import (
 )
 
 ROOT = Path(__file__).resolve().parent.parent
-#: A full result dict as bench.py assembled it (per-cell lists included):
-#: 20.5 KB as one line, too long for a reader that keeps only the tail.
-FULL = json.loads((ROOT / "reports" / "mi355x" / "bench_latest.json").read_text())
+#: A full result dict as bench.py assembled it before the per-cell lists moved
+#: to the report file (a fixture of bench.py's own output): 20.5 KB as one
+#: line, too long for a reader that keeps only the tail.
+FULL = json.loads((ROOT / "tests" / "golden" / "bench_result_full.json").read_text())
+#: The line the latest bench.py run printed.
+LATEST = ROOT / "reports" / "mi355x" / "bench_latest.json"
 
 
 def _full() -> dict:
@@ -116,3 +119,18 @@ def test_cells_report_layout() -> None:
     assert row["kernel_name"].endswith("_hip") and row["shape"] and row["dtype"] in ("float16", "bfloat16")
     assert rep["comparisons"] == comps
     assert rep["decoder"]["ako"]["prefill_ms"] == FULL["decoder"]["ako"]["prefill_ms"]
+
+
+def test_latest_recorded_line_is_within_the_contract() -> None:
+    """The committed line of the latest bench.py run: strict JSON under the
+    limit, with the headline keys, the roofline and the CPU baseline."""
+    text = LATEST.read_text().strip()
+    assert len(text) < LINE_LIMIT
+    line = _strict(text)
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in line, key
+    roof = line["roofline"]
+    assert roof["bound"] == "hbm" and 0 < roof["frac"] < 1
+    assert abs(roof["achieved"] / roof["peak"] - roof["frac"]) < 1e-3
+    assert line["cpu_baseline"]["kind"] in ("port", "reference") and line["cpu_baseline"]["cores"] >= 1
