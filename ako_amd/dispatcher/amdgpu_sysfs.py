@@ -122,10 +122,12 @@ def kfd_gpu_id(slot: str, topology: Path = KFD_TOPOLOGY) -> int | None:
 def kfd_processes(gpu_id: int | None = None, kfd_proc: Path = KFD_PROCS) -> list[int] | None:
     """PIDs with a KFD compute context, or None when the KFD is not visible.
 
-    With ``gpu_id``, only processes that hold something on that GPU: a
-    process directory lists per-GPU entries named ``<what>_<gpu_id>``
-    (``vram_``, ``sdma_``, ``stats_``); a directory with no per-GPU entries
-    at all is counted, since it cannot be ruled out."""
+    With ``gpu_id``, only processes with a per-device entry for that GPU: a
+    process directory lists entries named ``<what>_<gpu_id>`` (``vram_``,
+    ``sdma_``, ``stats_``) for each GPU it has opened, and a HIP process
+    typically opens every GPU it can see, so this rules out processes
+    confined to other GPUs (``HIP_VISIBLE_DEVICES``). A directory with no
+    per-device entries at all is counted, since it cannot be ruled out."""
     try:
         entries = [p for p in kfd_proc.iterdir() if p.name.isdigit()]
     except OSError:
