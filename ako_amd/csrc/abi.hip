@@ -176,6 +176,7 @@ int ako_set_tuning(int op, int key, int value) {
       break;
     case 2:
       if (key == 1) { ako::g_swiglu_tuning.vecs_per_thread = value; return AKO_OK; }
+      if (key == 2) { ako::g_swiglu_tuning.xcd_chunk = value; return AKO_OK; }
       break;
     default:
       break;

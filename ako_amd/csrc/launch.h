@@ -41,6 +41,7 @@ struct RopeTuning {
 };
 struct SwigluTuning {
   TuningKey vecs_per_thread{0};  // key 1: packets per lane (1, 2, 4 or 8)
+  TuningKey xcd_chunk{0};        // key 2: consecutive workgroups per XCD run in dense launches (0 or 1 = block order)
 };
 extern RmsTuning g_rms_tuning;
 extern RopeTuning g_rope_tuning;

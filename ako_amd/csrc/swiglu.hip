@@ -48,11 +48,11 @@ template <typename T, int U, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void swiglu_flat(const T* __restrict__ g,
                                                      const T* __restrict__ u, T* __restrict__ y,
                                                      int64_t first_packet, int64_t npackets,
-                                                     int64_t nelems) {
+                                                     int64_t nelems, XcdRuns runs) {
   constexpr int E = 16 / static_cast<int>(sizeof(T));
   using P = Pack<T, E>;
-  const int64_t base =
-      first_packet + static_cast<int64_t>(blockIdx.x) * (BLOCK * U) + threadIdx.x;
+  const int64_t base = first_packet +
+                       static_cast<int64_t>(block_order(blockIdx.x, gridDim.x, runs)) * (BLOCK * U) + threadIdx.x;
   P gv[U], uv[U];
 #pragma unroll
   for (int k = 0; k < U; ++k) {
@@ -128,11 +128,19 @@ hipError_t run_flat(const SwigluArgs& a, hipStream_t stream) {
   const int64_t npk = nelems / E;
   const int64_t per_block = int64_t(kBlock) * U;
   const int64_t blocks = std::max<int64_t>(1, ceil_div(npk, per_block));
+  // Workgroups go to the XCDs in block order unless key 2 asks for runs.
+  // Runs of 4 read +1.2 / +2.0 points of peak at M = 16384 / 4096 (bf16 x
+  // 14336) in one placement of the buffers, but over six placements (random
+  // spacers between the input copies, interleaved timings on MI355X) they
+  // averaged -0.2 points at M = 16384 (-0.8 to +0.1) and +0.7 at M = 4096
+  // (+0.3 to +1.5): not enough to change the default.
+  const int forced = g_swiglu_tuning.xcd_chunk;
+  const XcdRuns runs = make_xcd_runs(forced > 1 ? static_cast<unsigned>(forced) : 1u);
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
     const int64_t nb = std::min(kMaxBlocksPerLaunch, blocks - b0);
     hipLaunchKernelGGL((swiglu_flat<T, U, kBlock>), dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0,
                        stream, static_cast<const T*>(a.g), static_cast<const T*>(a.u),
-                       static_cast<T*>(a.y), b0 * per_block, npk, nelems);
+                       static_cast<T*>(a.y), b0 * per_block, npk, nelems, runs);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

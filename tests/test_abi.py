@@ -187,7 +187,7 @@ def test_tuning_keys(lib) -> None:
     assert lib.ako_set_tuning(9, 1, 1) == INVALID
     assert lib.ako_set_tuning(0, 1, -1) == INVALID
     assert lib.ako_set_tuning(0, 5, 3) == INVALID
-    assert lib.ako_set_tuning(2, 2, 256) == INVALID  # SwiGLU has one key: packets per lane
+    assert lib.ako_set_tuning(2, 3, 1) == INVALID  # SwiGLU has two keys: packets per lane, XCD runs
     assert lib.ako_set_tuning(0, 8, 3) == INVALID  # early weights: 0, 1 or 2
     assert lib.ako_set_tuning(0, 9, 3) == INVALID  # pipelined kernel: 0, 1 or 2
     assert lib.ako_set_tuning(0, 10, 33) == INVALID  # pipelined workgroups per CU: at most 32
@@ -195,7 +195,7 @@ def test_tuning_keys(lib) -> None:
     assert lib.ako_set_tuning(0, 12, 3) == INVALID  # write-through stores: 0, 1 or 2
     assert lib.ako_set_tuning(1, 4, 0) == INVALID  # RoPE has three keys
     for op, key in ((0, 1), (0, 2), (0, 3), (0, 4), (0, 5), (0, 6), (0, 7), (0, 8), (0, 9), (0, 10), (0, 11), (0, 12), (1, 1),
-                    (1, 2), (1, 3), (2, 1)):
+                    (1, 2), (1, 3), (2, 1), (2, 2)):
         assert lib.ako_set_tuning(op, key, 0) == OK
 
 

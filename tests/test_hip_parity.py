@@ -722,6 +722,27 @@ def test_swiglu_config4(m: int) -> None:
                   torch.bfloat16)
 
 
+def test_swiglu_xcd_runs_cover_every_packet() -> None:
+    """Dense SwiGLU with workgroups handed to the XCDs in runs (key 2): the
+    map is a bijection on the grid, so every run length, including ones that
+    leave a partial last round and trailing workgroups, gives the
+    block-order output bit for bit, and the tail elements past the last full
+    packet are still written."""
+    from ako_amd import _native
+
+    g = grandn((77, 14343), torch.bfloat16, 17, scale=4.0)
+    u = grandn((77, 14343), torch.bfloat16, 18)
+    try:
+        _native.set_tuning(2, 2, 1)
+        want = swiglu_hip(g, u)
+        assert_oracle(oracle.swiglu(to_np(g), to_np(u), dtype="bfloat16"), to_np(want), torch.bfloat16)
+        for chunk in (0, 2, 3, 4, 8, 64, 100000):
+            _native.set_tuning(2, 2, chunk)
+            assert torch.equal(swiglu_hip(g, u), want), chunk
+    finally:
+        _native.set_tuning(2, 2, 0)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(8, 2048, 5632), (2, 8448), (3, 1001), (1, 1), (7,), (4, 12)])
 def test_swiglu_shapes(shape, dtype) -> None:
