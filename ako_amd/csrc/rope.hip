@@ -145,26 +145,34 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
   if constexpr (!CACHE) load_tables();
   P lo[ITERS], hi[ITERS];
   T* dst[ITERS];
-  [[maybe_unused]] bool want[ITERS];
+  [[maybe_unused]] int64_t row_stride[ITERS];
+  [[maybe_unused]] bool first[ITERS];
   [[maybe_unused]] bool copy[ITERS];
-  // Without a cache the destination is known with the source, and each head
-  // group's addresses are formed right before its loads (forming them all
-  // after the loads measured 0.8 points of peak slower at (4, 2048)).
+  // Each head group's addresses are formed right before its loads (forming
+  // the destinations after all loads measured 0.8 points of peak slower at
+  // (4, 2048)). In KV-cache mode the destination row of k and v is the cache
+  // slot, known only once the position is read: the rest of the address is
+  // formed here and the row added after.
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int h = base + it * heads_per_iter + hl;
-    want[it] = lane_live && h < total;
     dst[it] = nullptr;
-    if (want[it]) {
+    if (lane_live && h < total) {
       const void* x = pick(h, a.t0.x, a.t1.x, a.t2.x);
       const int64_t sxb = pick(h, a.t0.sxb, a.t1.sxb, a.t2.sxb), sxs = pick(h, a.t0.sxs, a.t1.sxs, a.t2.sxs),
                     sxh = pick(h, a.t0.sxh, a.t1.sxh, a.t2.sxh);
-      const T* src = static_cast<const T*>(x) + b * sxb + s * sxs + head_in(h) * sxh + j * E;
-      if constexpr (!CACHE) {
-        void* y = pick(h, a.t0.y, a.t1.y, a.t2.y);
-        const int64_t syb = pick(h, a.t0.syb, a.t1.syb, a.t2.syb), sys = pick(h, a.t0.sys, a.t1.sys, a.t2.sys),
-                      syh = pick(h, a.t0.syh, a.t1.syh, a.t2.syh);
-        dst[it] = static_cast<T*>(y) + b * syb + s * sys + head_in(h) * syh + j * E;
+      const int64_t hh = head_in(h);
+      const T* src = static_cast<const T*>(x) + b * sxb + s * sxs + hh * sxh + j * E;
+      void* y = pick(h, a.t0.y, a.t1.y, a.t2.y);
+      const int64_t syb = pick(h, a.t0.syb, a.t1.syb, a.t2.syb), sys = pick(h, a.t0.sys, a.t1.sys, a.t2.sys),
+                    syh = pick(h, a.t0.syh, a.t1.syh, a.t2.syh);
+      if constexpr (CACHE) {
+        dst[it] = static_cast<T*>(y) + b * syb + hh * syh + j * E;
+        row_stride[it] = sys;
+        first[it] = h < a.t0.heads;
+        copy[it] = h >= h01;
+      } else {
+        dst[it] = static_cast<T*>(y) + b * syb + s * sys + hh * syh + j * E;
       }
       lo[it] = load_pack<T, E, true>(src);
       if constexpr (NEOX) hi[it] = load_pack<T, E, true>(src + half);
@@ -174,15 +182,9 @@ __global__ __launch_bounds__(kWave* TPB) void rope_vec(RopeDev a) {
     load_tables();
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-      const int h = base + it * heads_per_iter + hl;
-      const bool first = h < a.t0.heads;
-      if (want[it] && !(dropped && !first)) {
-        void* y = pick(h, a.t0.y, a.t1.y, a.t2.y);
-        const int64_t syb = pick(h, a.t0.syb, a.t1.syb, a.t2.syb), sys = pick(h, a.t0.sys, a.t1.sys, a.t2.sys),
-                      syh = pick(h, a.t0.syh, a.t1.syh, a.t2.syh);
-        dst[it] = static_cast<T*>(y) + b * syb + (first ? s : p) * sys + head_in(h) * syh + j * E;
-        copy[it] = h >= h01;
-      }
+      if (dst[it] == nullptr) continue;
+      if (dropped && !first[it]) dst[it] = nullptr;  // no cache slot for this token
+      else dst[it] += (first[it] ? s : p) * row_stride[it];
     }
   }
 #pragma unroll
