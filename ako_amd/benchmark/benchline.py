@@ -25,11 +25,13 @@ _CELL = re.compile(r"^(?P<op>[a-z_]+?)_(?P<dt>fp16|bf16|fp32)_(?P<shape>\d+(?:x\
 _DTYPES = {"fp16": "float16", "bf16": "bfloat16", "fp32": "float32"}
 
 #: Cells whose share of peak is held to the >= 75% prefill target, by op:
-#: RMSNorm rows = 16384, RoPE (4, 2048), SwiGLU M in {4096, 16384}.
+#: RMSNorm rows = 16384, RoPE (4, 2048) (also with the KV-cache write, as the
+#: decoder calls it), SwiGLU M in {4096, 16384}.
 PREFILL = {
     "rmsnorm": re.compile(r"^rmsnorm_(fp16|bf16)_16384x\d+$"),
     "rmsnorm_residual": re.compile(r"^rmsnorm_residual_(fp16|bf16)_16384x\d+$"),
     "rope_qk": re.compile(r"^rope_qk_(fp16|bf16)_4x2048$"),
+    "rope_qk_cache": re.compile(r"^rope_qk_cache_(fp16|bf16)_4x2048_q32_kv8$"),
     "rope_q": re.compile(r"^rope_q_(fp16|bf16)_4x2048x32x128$"),
     "swiglu": re.compile(r"^swiglu_bf16_(4096|16384)x14336$"),
 }
