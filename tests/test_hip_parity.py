@@ -609,6 +609,8 @@ CACHE_CASES = [
     (2, 5, 8, 2, 128, 3, 16),       # GQA, several tokens at once
     (1, 4, 4, 4, 6, 0, 8),          # head_dim 6: the scalar kernel
     (1, 3, 2, 2, 64, 6, 8),         # the last token's slot (8) is past the cache: dropped
+    (1, 512, 32, 32, 128, 0, 640),  # configs[4] prefill: 6144 wavefronts, four per workgroup
+    (2, 300, 32, 8, 128, 20, 310),  # GQA prefill at an offset, the last 10 tokens past the cache
 ]
 
 
