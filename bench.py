@@ -32,7 +32,8 @@ The printed line (one JSON object, kept under 8 KB) also carries:
   rope_prefill  RoPE at (4, 2048) as the fused q+k launch, and as the
                 decoder's own prefill call, which also writes k and v into
                 its KV cache (qk_cache);
-  prefill_floor per op, the prefill cell with the lowest share of peak.
+  prefill_floor per op, the prefill cell with the lowest share of peak,
+                timed back to back.
 
 Every timed cell goes to ``--cells-out`` (reports/mi355x/bench_cells.json by
 default) in the reference's report layout, with the selection's rows:

@@ -94,6 +94,9 @@ def test_prefill_floor_picks_the_lowest_prefill_cell() -> None:
     assert floor["swiglu"]["cells"] == 2 and floor["rope_qk"]["cells"] == 2
     lows = [r for r in FULL["extras"] if r["name"] in ("rope_qk_fp16_4x2048", "rope_qk_bf16_4x2048")]
     assert floor["rope_qk"]["min_pct"] == min(r["pct_hbm_peak"] for r in lows)
+    # The step's cells count by their back-to-back figure, not the per-launch events.
+    step = [r for r in FULL["per_kernel"] if r["name"].startswith("rmsnorm_fp16") or r["name"].startswith("rmsnorm_bf16")]
+    assert floor["rmsnorm"]["min_pct"] == min(r["back_to_back"]["pct_hbm_peak"] for r in step)
     # decode cells never count
     for v in floor.values():
         shape = parse_cell(v["cell"])["shape"]
