@@ -37,7 +37,7 @@ struct RmsTuning {
 struct RopeTuning {
   TuningKey tokens_per_block{0};  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)
   TuningKey iters{0};             // key 2: head chunks unrolled per loop trip
-  TuningKey xcd_chunk{0};         // key 3: consecutive workgroups per XCD run (0 or 1 = block order)
+  TuningKey xcd_chunk{0};         // key 3: consecutive workgroups per XCD run (1 = block order; 0 = runs of 128 for one tensor from 8192 workgroups)
 };
 struct SwigluTuning {
   TuningKey vecs_per_thread{0};  // key 1: packets per lane (1, 2, 4 or 8)
