@@ -32,7 +32,7 @@ struct RmsTuning {
   TuningKey pipeline{0};         // key 9: 1 = never the pipelined persistent kernel, 2 = whenever eligible (0 = heuristic)
   TuningKey pipe_blocks_per_cu{0};  // key 10: workgroups per CU in the pipelined grid (0 = 16 wavefronts per CU)
   TuningKey load_groups{0};      // key 11: residual (16, 2) rows: 1 = both packets per load group, 2 = one (0 = one with write-through stores, else by dtype)
-  TuningKey write_through{0};    // key 12: (16, 2) and (16, 1) rows: 1 = non-temporal stores, 2 = write-through stores (0 = write-through on (16, 2), and bf16 residual (16, 1), launches of many rows)
+  TuningKey write_through{0};    // key 12: (16, 2) and (16, 1) rows: 1 = non-temporal stores, 2 = write-through stores (0 = write-through on (16, 2) launches of many rows)
 };
 struct RopeTuning {
   TuningKey tokens_per_block{0};  // key 1: wavefronts per workgroup (1, 2, 4, 8 or 16; one group per wavefront)

@@ -586,8 +586,15 @@ constexpr unsigned kXcdChunk = 8;
 // of 8 (e.g. 81.5% / 82.7% against 80.3% / 81.3%, bf16 / fp16); runs of 12,
 // 20, 24 and 32 were no better than 8, and the whole 12-launch step read
 // 6542 against 6525 GB/s. Plain rows of 16384 and residual rows of 8192
-// showed no consistent gain from 16 and keep 8.
+// showed no consistent gain from 16.
 constexpr unsigned kXcdChunkWideResidual = 16;
+// Plain rows of 16384 half elements take runs of 4. Five buffer placements
+// (random spacer allocations between the input copies) on each of three
+// MI355X boxes, variants interleaved, medians of settled back-to-back runs:
+// against runs of 8, fp16 +0.29 to +0.30 points of peak (per-placement
+// -0.06 to +0.71), bf16 +0.56 to +0.70 (+0.20 to +0.97); runs of 16 were
+// -0.23 to -0.29.
+constexpr unsigned kXcdChunkWidePlain = 4;
 
 // Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
 // the dispatch packet never wraps; larger problems take several launches,
@@ -609,13 +616,15 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   // such rows per CU exceed the CU's share of its XCD's L2 (4 MiB / 32 CUs),
   // so an LDS reservation above half the CU's 160 KiB limits those launches to
   // one 16-wavefront workgroup per CU (measured +1-3% at 16384 x 16384).
-  const bool one_per_cu = RES && WPR == 16 && a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024;
+  const bool row32k = a.hidden * static_cast<int64_t>(sizeof(T)) >= 32 * 1024;
+  const bool one_per_cu = RES && WPR == 16 && row32k;
   unsigned lds = static_cast<unsigned>(g_rms_tuning.lds_reserve);
   if (lds == 0 && one_per_cu) lds = 82 * 1024;
-  const unsigned run = one_per_cu && VPT == 2 && sizeof(T) == 2 ? kXcdChunkWideResidual : kXcdChunk;
+  unsigned run = kXcdChunk;
+  if (WPR == 16 && VPT == 2 && sizeof(T) == 2 && row32k) run = RES ? kXcdChunkWideResidual : kXcdChunkWidePlain;
   // Default: rows of >= 16 KiB go to the XCDs in runs of 8 consecutive rows
-  // (16 for the residual rows of 16384 half elements; once the launch holds 8
-  // such runs); narrower rows keep block order.
+  // (rows of 16384 half elements: 16 residual, 4 plain; once the launch
+  // holds 8 such runs); narrower rows keep block order.
   // Medians of 5 cold runs on MI355X, 16384 rows, fp16/bf16, against block
   // order: +1% at 16 KiB rows, +4% (plain) and +8-10% (residual) at 32 KiB
   // rows, -1-2% at 8 KiB rows; whole-grid runs (chunk = n / 8) lose up to 12%
@@ -667,15 +676,16 @@ hipError_t run_reg(const RmsArgs& a, hipStream_t stream) {
   // -3.5% fp16).
   // Rows of 8193-16384 elements at 16 wavefronts x 2 packets in launches of
   // many rows store write-through (see store_write_through); residual rows
-  // then take one packet per load group, fp16 and bf16 alike. So do bf16
-  // residual rows at 16 wavefronts x 1 packet (4097-8192 elements): medians
-  // of 7 interleaved rotating runs on MI355X, 16384 x 8192, three boxes, +0.7
-  // to +0.9 points of peak (78.0 -> 78.9%); fp16 rows there were -0.5 to +0.2
-  // and keep non-temporal stores. fp32 rows of 8192 on the (16, 2) shape:
-  // plain 80.6% against 78.2% with non-temporal stores, residual 82.5%
-  // against 81.2%.
+  // then take one packet per load group, fp16 and bf16 alike. fp32 rows of
+  // 8192 on the same shape: plain 80.6% against 78.2% with non-temporal
+  // stores, residual 82.5% against 81.2%. Rows at 16 wavefronts x 1 packet
+  // (4097-8192 elements) keep non-temporal stores by default: residual rows
+  // of 8192, five buffer placements on each of three MI355X boxes, variants
+  // interleaved, write-through was -0.43 to -0.55 points of peak for bf16
+  // (every placement -0.17 or worse) and -0.33 to -0.42 for fp16. Key 12 = 2
+  // still selects it there.
   if constexpr ((VPT == 2 || VPT == 1) && WPR == 16) {
-    constexpr bool kWtByDefault = VPT == 2 || (RES && std::is_same_v<T, __bf16>);
+    constexpr bool kWtByDefault = VPT == 2;
     const int wt_forced = g_rms_tuning.write_through;
     if (wt_forced == 2 || (wt_forced == 0 && kWtByDefault && a.rows > kFewRows)) {
       if constexpr (RES) {

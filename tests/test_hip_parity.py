@@ -346,7 +346,8 @@ def test_rmsnorm_write_through_stores_match(dtype, w_dtype, h, stride) -> None:
     non-temporal stores (key 12 = 1), residual rows with either load grouping:
     the same values in the same places, so bit-identical outputs, also where
     lanes sit idle and where input rows are padded; the default
-    (write-through from 257 rows) against the oracle on sampled rows."""
+    (write-through from 257 rows on (16, 2), non-temporal on (16, 1)) against
+    the oracle on sampled rows."""
     from ako_amd import _native
 
     try:
@@ -1159,8 +1160,9 @@ def _assert_same_bits(got: torch.Tensor, ref_bits: np.ndarray, what: str) -> Non
 
 # (hidden, rows of the 524288 pairs repeated `copies` times): the residual
 # sum through each kernel that adds packets: rmsnorm_reg at (8, 1) with early
-# weights and through rmsnorm_pipe (4096), at (16, 1) with non-temporal and,
-# from 257 rows, write-through stores (8192), at (16, 2) (16384), and
+# weights and through rmsnorm_pipe (4096), at (16, 1) (8192), at (16, 2)
+# (16384; from 257 rows with write-through stores and one packet per load
+# group), and
 # rmsnorm_stream for rows past the register budget (131072).
 BF16_SUM_CASES = [(4096, 1), (4096, 3), (8192, 1), (8192, 5), (16384, 1), (16384, 9), (131072, 1)]
 
