@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "ako_swiglu_fwd": (_int, [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _int, _ptr]),
     "ako_set_tuning": (_int, [_int, _int, _int]),
+    "ako_time_next_launch": (_int, [_ptr, _ptr]),
 }
 
 
@@ -199,6 +200,25 @@ def check(status: int, fn_name: str) -> None:
 
 def set_tuning(op: int, key: int, value: int) -> None:
     check(load().ako_set_tuning(op, key, value), "ako_set_tuning")
+
+
+def time_next_launch(start: "torch.cuda.Event", stop: "torch.cuda.Event") -> None:
+    """Bind ``start`` and ``stop`` to the next kernel launch this thread makes
+    through the library (``ako_time_next_launch``): their elapsed time is then
+    that kernel's own duration. Each event must have been recorded once
+    before, so that torch has created it."""
+    handles = (int(start.cuda_event), int(stop.cuda_event))
+    if not all(handles):
+        raise ValueError("time_next_launch: record each event once before arming it")
+    check(load().ako_time_next_launch(*handles), "ako_time_next_launch")
+
+
+def disarm_launch_timing() -> bool:
+    """Drop an armed event pair; True when one was still armed (no launch took it)."""
+    status = load().ako_time_next_launch(None, None)
+    if status not in (0, 1):
+        check(status, "ako_time_next_launch")
+    return status == 1
 
 
 def current_stream(device: torch.device) -> int:

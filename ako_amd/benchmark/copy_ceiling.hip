@@ -15,13 +15,16 @@
 //    "us": t, "gbps": 2N/t, "frac": gbps/8000}
 // Buffers rotate through a 2 GiB source pool and a 2 GiB destination pool, so
 // consecutive launches never find their data in the 256 MB MALL or the L2s.
-// The 25 launches of a size are queued back to back, each between its own
-// pair of events, behind a short spin kernel that keeps the device busy while
-// they are queued, and the stream is synchronised once at the end (as
-// bench.py times each launch), so the host's launch latency is not counted;
-// the median of the last 22 is reported as "us". The same 22 launches are
-// then queued again between one pair of events around all of them (as
-// bench.py times its extra cells), and the mean is reported as "b2b_us".
+// The 25 launches of a size are queued back to back, each with its own pair
+// of events bound to the launch (hipExtLaunchKernelGGL: the events take the
+// dispatch's own start and end, with no marker packets between the copies),
+// behind a short spin kernel that keeps the device busy while they are
+// queued, and the stream is synchronised once at the end (as bench.py times
+// each launch); the median of the last 22 is reported as "us". The same 22
+// launches are then queued again between one pair of events around all of
+// them (as bench.py times its extra cells), and the mean is reported as
+// "b2b_us".
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -57,6 +60,17 @@ __global__ __launch_bounds__(BLOCK) void copy_packets(const u32x4* __restrict__ 
     } else {
       asm volatile("global_store_dwordx4 %0, %1, off sc1 nt\n\ts_nop 0" : : "v"(b + i), "v"(v));
     }
+  }
+}
+
+// One copy launch; with events, they are bound to it (its start and end).
+template <int BLOCK, int STORE>
+void launch_copy(long n, const u32x4* a, u32x4* b, hipEvent_t start, hipEvent_t stop) {
+  const dim3 grid((n + BLOCK - 1) / BLOCK);
+  if (start != nullptr) {
+    hipExtLaunchKernelGGL((copy_packets<BLOCK, STORE>), grid, dim3(BLOCK), 0, 0, start, stop, 0u, a, b, n);
+  } else {
+    hipLaunchKernelGGL((copy_packets<BLOCK, STORE>), grid, dim3(BLOCK), 0, 0, a, b, n);
   }
 }
 
@@ -109,33 +123,28 @@ int main(int argc, char** argv) {
     for (int variant = 0; variant < 4; ++variant) {
       const int block = variant % 2 ? 1024 : 256;
       const int store = variant / 2;
-      const auto launch = [&](int rep) {
+      const auto launch = [&](int rep, hipEvent_t ev0, hipEvent_t ev1) {
         const long off = (rep % slots) * bytes;
         const u32x4* a = reinterpret_cast<const u32x4*>(src + off);
         u32x4* b = reinterpret_cast<u32x4*>(dst + off);
-        const dim3 grid((n + block - 1) / block);
-        if (variant == 0) hipLaunchKernelGGL((copy_packets<256, 0>), grid, dim3(256), 0, 0, a, b, n);
-        if (variant == 1) hipLaunchKernelGGL((copy_packets<1024, 0>), grid, dim3(1024), 0, 0, a, b, n);
-        if (variant == 2) hipLaunchKernelGGL((copy_packets<256, 1>), grid, dim3(256), 0, 0, a, b, n);
-        if (variant == 3) hipLaunchKernelGGL((copy_packets<1024, 1>), grid, dim3(1024), 0, 0, a, b, n);
+        if (variant == 0) launch_copy<256, 0>(n, a, b, ev0, ev1);
+        if (variant == 1) launch_copy<1024, 0>(n, a, b, ev0, ev1);
+        if (variant == 2) launch_copy<256, 1>(n, a, b, ev0, ev1);
+        if (variant == 3) launch_copy<1024, 1>(n, a, b, ev0, ev1);
         CHECK(hipGetLastError());
       };
       hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, 0, kLeadCycles);
       CHECK(hipGetLastError());
-      for (int rep = 0; rep < kReps; ++rep) {
-        CHECK(hipEventRecord(start[rep]));
-        launch(rep);
-        CHECK(hipEventRecord(stop[rep]));
-      }
+      for (int rep = 0; rep < kReps; ++rep) launch(rep, start[rep], stop[rep]);
       CHECK(hipDeviceSynchronize());
       // Back to back: the timed launches again, one event pair around them all,
       // behind the spin and the kWarm untimed launches (their own slots), so
       // the first timed launch follows copies as every later one does.
       hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, 0, kLeadCycles);
       CHECK(hipGetLastError());
-      for (int rep = 0; rep < kWarm; ++rep) launch(rep);
+      for (int rep = 0; rep < kWarm; ++rep) launch(rep, nullptr, nullptr);
       CHECK(hipEventRecord(start[0]));
-      for (int rep = kWarm; rep < kReps; ++rep) launch(rep);
+      for (int rep = kWarm; rep < kReps; ++rep) launch(rep, nullptr, nullptr);
       CHECK(hipEventRecord(stop[0]));
       CHECK(hipDeviceSynchronize());
       float b2b_ms = 0.f;

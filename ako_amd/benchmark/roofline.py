@@ -160,10 +160,19 @@ LEAD_PASSES = 3
 
 
 def time_each_launch(
-    calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int, lead_passes: int = LEAD_PASSES
+    calls: Sequence[tuple[str, int, Callable[[], Any]]], *, steps: int, lead_passes: int = LEAD_PASSES,
+    kernel_events: bool = False,
 ) -> list[LaunchStats]:
-    """Per-launch device durations: an event pair around every launch of
+    """Per-launch device durations: an event pair for every launch of
     ``steps`` passes over ``calls`` (name, alg_bytes, thunk).
+
+    By default the pair is recorded around the call (a marker packet on each
+    side of the kernel). With ``kernel_events`` each thunk must make exactly
+    one launch through the kernel library, and the pair is bound to that
+    launch's own dispatch (``ako_time_next_launch``): the elapsed time is the
+    kernel's start-to-end time, the duration a kernel trace records, and no
+    marker packets sit between the kernels. A thunk that made no library
+    launch raises.
 
     ``lead_passes`` untimed passes over the same calls are queued ahead of
     the timed ones without a wait, so the first timed launch follows the same
@@ -175,16 +184,31 @@ def time_each_launch(
     stream = torch.cuda.current_stream()
     marks = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in calls] for _ in range(steps)]
+    if kernel_events:
+        from ako_amd import _native
+
+        # torch creates an event at its first record; record every one now,
+        # outside the timed passes, so that each has a handle to arm.
+        for pairs in marks:
+            for ev0, ev1 in pairs:
+                ev0.record(stream)
+                ev1.record(stream)
     torch.cuda.synchronize()
     queue_lead()
     for _ in range(lead_passes):
         for _, _, fn in calls:
             fn()
     for step in range(steps):
-        for (_, _, fn), (ev0, ev1) in zip(calls, marks[step]):
-            ev0.record(stream)
-            fn()
-            ev1.record(stream)
+        for (name, _, fn), (ev0, ev1) in zip(calls, marks[step]):
+            if kernel_events:
+                _native.time_next_launch(ev0, ev1)
+                fn()
+                if _native.disarm_launch_timing():
+                    raise RuntimeError(f"time_each_launch: {name} made no launch through the kernel library")
+            else:
+                ev0.record(stream)
+                fn()
+                ev1.record(stream)
     torch.cuda.synchronize()
     stats: dict[str, LaunchStats] = {}
     for step in range(steps):

@@ -124,6 +124,20 @@ int ako_device_identity(int device, char* buf, int64_t buf_len) {
   return AKO_OK;
 }
 
+int ako_time_next_launch(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(AKO_ERR_INVALID_ARGUMENT, "ako_time_next_launch: start and stop must both be set or both be NULL");
+  ako::ArmedEvents& slot = ako::armed_events();
+  if (start_event == nullptr) {
+    const bool pending = slot.start != nullptr;
+    slot = ako::ArmedEvents{};
+    return pending ? 1 : AKO_OK;
+  }
+  slot.start = static_cast<hipEvent_t>(start_event);
+  slot.stop = static_cast<hipEvent_t>(stop_event);
+  return AKO_OK;
+}
+
 int ako_set_tuning(int op, int key, int value) {
   if (value < 0) return fail(AKO_ERR_INVALID_ARGUMENT, "tuning value must be >= 0, got %d", value);
   switch (op) {

@@ -4,12 +4,47 @@
 // the chosen path requires, strides consistent.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <atomic>
 
 namespace ako {
+
+// A start/stop event pair armed by ako_time_next_launch on one host thread.
+// The next kernel launch that thread makes through AKO_LAUNCH takes the pair
+// (and disarms it): it goes out through hipExtLaunchKernelGGL, which binds
+// both events to the dispatch itself, so their elapsed time is the kernel's
+// own start-to-end time, with no marker packets queued around it. Launches
+// without an armed pair are plain hipLaunchKernelGGL launches.
+struct ArmedEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+inline ArmedEvents& armed_events() {
+  thread_local ArmedEvents pair;
+  return pair;
+}
+inline ArmedEvents take_armed_events() {
+  ArmedEvents& slot = armed_events();
+  const ArmedEvents taken = slot;
+  slot = ArmedEvents{};
+  return taken;
+}
+
+// hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...), or the same
+// launch carrying the thread's armed event pair. A kernel name with template
+// arguments goes in parentheses, as for hipLaunchKernelGGL.
+#define AKO_LAUNCH(kernel, grid, block, lds, stream, ...)                                              \
+  do {                                                                                                 \
+    const ::ako::ArmedEvents ako_events_ = ::ako::take_armed_events();                                 \
+    if (ako_events_.start != nullptr)                                                                  \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ako_events_.start, ako_events_.stop, 0u, \
+                            __VA_ARGS__);                                                              \
+    else                                                                                               \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                               \
+  } while (0)
 
 enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 

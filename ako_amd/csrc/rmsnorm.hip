@@ -636,7 +636,7 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
     const int order = g_rms_tuning.row_order, chunk = g_rms_tuning.xcd_chunk;
     if (order == 1) xcd_chunk = 1;
     if (order == 2) xcd_chunk = chunk > 0 ? unsigned(chunk) : unsigned(grid.x / 8);
-    hipLaunchKernelGGL((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, EW, SPLIT, WT>),
+    AKO_LAUNCH((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, EW, SPLIT, WT>),
                        grid, block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                        static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
                        b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
@@ -748,7 +748,7 @@ template <typename T, typename W, int WPR, int VPT, bool RES>
 hipError_t run_pipe(const RmsArgs& a, hipStream_t stream) {
   const int64_t blocks = pipe_blocks(WPR, RES, a.rows);
   const int xcd_runs = g_rms_tuning.row_order == 1 ? 0 : 1;
-  hipLaunchKernelGGL((rmsnorm_pipe<T, W, WPR, VPT, RES>), dim3(static_cast<unsigned>(blocks)), dim3(kWave * WPR),
+  AKO_LAUNCH((rmsnorm_pipe<T, W, WPR, VPT, RES>), dim3(static_cast<unsigned>(blocks)), dim3(kWave * WPR),
                      0, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                      static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout), a.rows, a.sx,
                      a.sr, a.sy, a.srout, 1.0f / static_cast<float>(a.hidden), a.eps, xcd_runs);
@@ -810,10 +810,10 @@ hipError_t run_stream(const RmsArgs& a, hipStream_t stream) {
   for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
     if (a.vector_ok) {
-      hipLaunchKernelGGL((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
+      AKO_LAUNCH((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
                          stream, x, r, w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
     } else {
-      hipLaunchKernelGGL((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
+      AKO_LAUNCH((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
                          w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
     }
     const hipError_t err = hipGetLastError();
@@ -870,12 +870,12 @@ hipError_t run_shard_partial(const RmsShardArgs& a, hipStream_t stream) {
   for (int64_t r0 = 0; r0 < a.rows; r0 += cap) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
     if (a.vector_ok) {
-      hipLaunchKernelGGL((rmsnorm_shard_partial<T, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
+      AKO_LAUNCH((rmsnorm_shard_partial<T, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
                          stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                          static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
                          a.sr, a.srout);
     } else {
-      hipLaunchKernelGGL((rmsnorm_shard_partial<T, 1, RES>), grid, dim3(kStreamBlock), 0, stream,
+      AKO_LAUNCH((rmsnorm_shard_partial<T, 1, RES>), grid, dim3(kStreamBlock), 0, stream,
                          static_cast<const T*>(a.x), static_cast<const T*>(a.r),
                          static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
                          a.sr, a.srout);
@@ -894,12 +894,12 @@ hipError_t run_shard_apply_r(const RmsShardArgs& a, hipStream_t stream) {
     const int64_t end = std::min(a.rows, r0 + cap);
     const dim3 grid(static_cast<unsigned>(ceil_div(end - r0, R)));
     if (a.vector_ok) {
-      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 16 / sizeof(T), R>), grid, dim3(kStreamBlock), 0,
+      AKO_LAUNCH((rmsnorm_shard_apply<T, W, 16 / sizeof(T), R>), grid, dim3(kStreamBlock), 0,
                          stream, static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
                          static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
                          a.eps);
     } else {
-      hipLaunchKernelGGL((rmsnorm_shard_apply<T, W, 1, R>), grid, dim3(kStreamBlock), 0, stream,
+      AKO_LAUNCH((rmsnorm_shard_apply<T, W, 1, R>), grid, dim3(kStreamBlock), 0, stream,
                          static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
                          static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
                          a.eps);

@@ -309,7 +309,7 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
     if (forced > 0) chunk = static_cast<unsigned>(forced);
     else if (one_tensor && grid.x >= kRunsMinBlocks) chunk = kRun;
     part.runs = make_xcd_runs(chunk);
-    hipLaunchKernelGGL((rope_vec<T, TT, NEOX, ITERS, TPB, CACHE>), grid, dim3(kWave * TPB), 0,
+    AKO_LAUNCH((rope_vec<T, TT, NEOX, ITERS, TPB, CACHE>), grid, dim3(kWave * TPB), 0,
                        stream, part);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -369,11 +369,11 @@ hipError_t run_typed(const RopeArgs& a, hipStream_t stream) {
   const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(pairs, 256), 1 << 16));
   const dim3 grid(blocks), block(256);
   if (a.pos != nullptr) {
-    if (a.neox) hipLaunchKernelGGL((rope_scalar<T, TT, true, true>), grid, block, 0, stream, d);
-    else hipLaunchKernelGGL((rope_scalar<T, TT, false, true>), grid, block, 0, stream, d);
+    if (a.neox) AKO_LAUNCH((rope_scalar<T, TT, true, true>), grid, block, 0, stream, d);
+    else AKO_LAUNCH((rope_scalar<T, TT, false, true>), grid, block, 0, stream, d);
   } else {
-    if (a.neox) hipLaunchKernelGGL((rope_scalar<T, TT, true, false>), grid, block, 0, stream, d);
-    else hipLaunchKernelGGL((rope_scalar<T, TT, false, false>), grid, block, 0, stream, d);
+    if (a.neox) AKO_LAUNCH((rope_scalar<T, TT, true, false>), grid, block, 0, stream, d);
+    else AKO_LAUNCH((rope_scalar<T, TT, false, false>), grid, block, 0, stream, d);
   }
   return hipGetLastError();
 }

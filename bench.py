@@ -12,8 +12,10 @@ elapsed device time, in GB/s.
 
 The printed line (one JSON object, kept under 8 KB) also carries:
   roofline      the dominant kernel (the slowest launch of the step) with its
-                per-launch duration from HIP events on the launch stream, and
-                a plain device copy of the same byte count timed the same way
+                per-launch duration from HIP events on the launch stream,
+                bound to each launch's dispatch (the kernel's own start and
+                end, no marker packets between launches), and a plain device
+                copy of the same byte count timed the same way
                 (copy_same_bytes: what the plainest stream of those bytes
                 reaches; a reference, which a kernel can pass);
   cpu_baseline  the reference's unfused PyTorch path on host CPU tensors with
@@ -38,7 +40,7 @@ The printed line (one JSON object, kept under 8 KB) also carries:
 Every timed cell goes to ``--cells-out`` (reports/mi355x/bench_cells.json by
 default) in the reference's report layout, with the selection's rows:
   per_kernel    every launch of the step, each beside its copy ceiling, by
-                per-launch events (as the roofline) and, under back_to_back,
+                launch-bound events (as the roofline) and, under back_to_back,
                 on its own as 60 launches between one event pair over cold
                 input copies, beside a copy timed the same way;
   extras        the RoPE and SwiGLU cells, the
@@ -110,7 +112,7 @@ class CopyCeilings:
 
     def annotate(self, row: dict, gbps: float, *, back_to_back: bool = False) -> None:
         """Add the copy's share of peak and the kernel's rate over the copy's,
-        the copy timed the way the row was (per-launch events, or one event
+        the copy timed the way the row was (launch-bound events, or one event
         pair around back-to-back launches)."""
         copy = self.get(row["alg_bytes"])
         if copy is None:
@@ -146,9 +148,9 @@ def headline(args, torch, rf, dev, peak, rnd):
     rf.warm(calls, args.warmup)
     total_ms = rf.time_steps(calls, steps=args.steps)
     # The dominant kernel's launch duration: the same K steps again, now with an
-    # event pair around every launch (kept out of the region above so that the
-    # step time holds nothing but the kernels and their launches).
-    per_launch = rf.time_each_launch(calls, steps=args.steps)
+    # event pair bound to every launch (hipExtLaunchKernelGGL through
+    # ako_time_next_launch: each pair holds its kernel's own start and end).
+    per_launch = rf.time_each_launch(calls, steps=args.steps, kernel_events=True)
     del calls
     torch.cuda.empty_cache()
     return bytes_per_step, total_ms, per_launch
@@ -627,7 +629,7 @@ def main() -> int:
         "alg_bytes_per_launch": dominant.alg_bytes,
         "mean_launch_us": round(dominant.mean_ms * 1e3, 2),
         "launches_timed": len(dominant.durations_ms),
-        "timing": "HIP events around each launch on the launch stream, over the same K steps as value",
+        "timing": "HIP events bound to each launch (hipExtLaunchKernelGGL) on the launch stream, over K steps as value",
         # Which launches of this kernel (0-based, counted over the process) carry
         # the event pairs: after the warm-up passes, the K steps of `value` and
         # the lead passes. A kernel trace of the same run can be cut to exactly
@@ -651,7 +653,7 @@ def main() -> int:
             "frac": copy["frac"],
             "kernel_over_copy": round(dominant.gbps() / copy["gbps"], 4),
             "source": f"ako_amd/_lib/copy_ceiling {copy['bytes_per_buffer']}: 16-byte-packet copy, cold "
-                      f"buffers, per-launch events, {copy['block']}-lane groups, {copy.get('store', 'nt')} stores",
+                      f"buffers, launch-bound events, {copy['block']}-lane groups, {copy.get('store', 'nt')} stores",
         }
         log(f"copy of the same bytes: {copy['gbps']:.0f} GB/s; the dominant kernel runs at "
             f"{100 * dominant.gbps() / copy['gbps']:.1f}% of it")

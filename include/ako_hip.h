@@ -214,6 +214,23 @@ int ako_swiglu_fwd(const void* gate, const void* up, void* y,
  */
 int ako_set_tuning(int op, int key, int value);
 
+/*
+ * Timing hook for benchmarks (no counterpart in the reference, which timed
+ * through Triton's do_bench): arms two HIP events for the next kernel launch
+ * that the calling host thread makes through any entry point above. That
+ * launch goes out through hipExtLaunchKernelGGL with the pair, which binds
+ * both events to the dispatch itself: hipEventElapsedTime(start, stop) is
+ * then the kernel's own start-to-end time, the figure a kernel trace reports,
+ * without the marker packets that an hipEventRecord on each side would queue
+ * around it. The events are the caller's (hipEventCreate, timing enabled);
+ * an entry point that makes several launches (inputs past 2^31 work-items)
+ * times its first. Arming replaces a pair that no launch has taken.
+ * start and stop both NULL disarms: the return value is then 1 when a pair
+ * was still armed (no launch took it), else AKO_OK. Exactly one NULL is
+ * AKO_ERR_INVALID_ARGUMENT.
+ */
+int ako_time_next_launch(void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif

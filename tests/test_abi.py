@@ -199,6 +199,27 @@ def test_tuning_keys(lib) -> None:
         assert lib.ako_set_tuning(op, key, 0) == OK
 
 
+def test_launch_timing_hook_arms_and_disarms(lib) -> None:
+    """ako_time_next_launch stores the pair for the calling thread only and
+    touches no HIP state: one NULL of the two is refused, disarming reports
+    whether a pair was still armed, and a pair armed on another thread is not
+    seen here."""
+    import threading
+
+    assert lib.ako_time_next_launch(A, None) == INVALID
+    assert "both" in _native.last_error()
+    assert lib.ako_time_next_launch(None, B) == INVALID
+    assert lib.ako_time_next_launch(None, None) == OK  # nothing armed
+    assert lib.ako_time_next_launch(A, B) == OK
+    assert lib.ako_time_next_launch(C, D) == OK  # replaces the unused pair
+    assert lib.ako_time_next_launch(None, None) == 1
+    assert lib.ako_time_next_launch(None, None) == OK
+    other = threading.Thread(target=lambda: lib.ako_time_next_launch(A, B))
+    other.start()
+    other.join()
+    assert lib.ako_time_next_launch(None, None) == OK
+
+
 def test_status_codes_become_python_exceptions() -> None:
     with pytest.raises(ValueError, match="ako_x"):
         _native.check(INVALID, "ako_x")
