@@ -68,8 +68,9 @@ struct WeightPacket {
 // runs of two builds, back to back: plain rows +1.5 (fp16) and +2.7 (bf16)
 // points of peak, residual fp16 rows +0.8 with one packet per load group
 // (with whole groups, -1.6), residual bf16 unchanged; rows of 8 KiB or less
-// were slower (pipelined 16 KiB-input rows: 82-87% down to 69-70%), so only
-// the (16, 2) shape and the bf16 residual rows of the (16, 1) shape use it.
+// were slower (pipelined 16 KiB-input rows: 82-87% down to 69-70%), so by
+// default only the (16, 2) shape uses it (key 12 = 2 selects it on (16, 1)
+// rows too).
 constexpr int kRawBufferWord3 = 0x00020000;  // raw (untyped) access, gfx9 CDNA layout
 constexpr int kStoreSc1Nt = 18;              // cache policy bits: nt (2) | sc1 (16)
 

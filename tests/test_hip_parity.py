@@ -211,14 +211,15 @@ def test_rmsnorm_xcd_row_orders_cover_every_row(rows: int) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows", [127, 130, 257, 1000, 2051])
-def test_rmsnorm_wide_residual_runs_of_16_cover_every_row(rows: int, dtype: torch.dtype) -> None:
-    """Residual rows of 16384 half elements go to the XCDs in runs of 16 rows
-    from 128 workgroups up (runs of 8 below that). Row counts straddle both
-    thresholds and the 256-row switch to write-through stores, and 1000 / 2051
-    leave partial runs and trailing blocks; the default order must give
-    bit-identical outputs to block order, which is checked against the oracle
-    on the first and last rows."""
+@pytest.mark.parametrize("rows", [31, 33, 127, 130, 257, 1000, 2051])
+def test_rmsnorm_wide_rows_xcd_runs_cover_every_row(rows: int, dtype: torch.dtype) -> None:
+    """Rows of 16384 half elements go to the XCDs in runs: residual rows in
+    runs of 16 from 128 workgroups up (runs of 8 from 64, block order below),
+    plain rows in runs of 4 from 32 workgroups up (block order below). Row
+    counts straddle those thresholds and the 256-row switch to write-through
+    stores, and 1000 / 2051 leave partial runs and trailing blocks; the
+    default order must give bit-identical outputs to block order, which is
+    checked against the oracle on the first and last rows."""
     from ako_amd import _native
 
     x = grandn((rows, 16384), dtype, 40)
@@ -228,14 +229,19 @@ def test_rmsnorm_wide_residual_runs_of_16_cover_every_row(rows: int, dtype: torc
     try:
         _native.set_tuning(0, 5, 1)
         base_y, base_s = rmsnorm_residual_hip(x, r, w)
+        base_p = rmsnorm_hip(x, w)
     finally:
         _native.set_tuning(0, 5, 0)
     y, s = rmsnorm_residual_hip(x, r, w)
     assert torch.equal(y, base_y) and torch.equal(s, base_s)
-    for sl in (slice(0, 48), slice(rows - 48, rows)):
+    p = rmsnorm_hip(x, w)
+    assert torch.equal(p, base_p)
+    n = min(48, rows)
+    for sl in (slice(0, n), slice(rows - n, rows)):
         ey, es = oracle.rmsnorm_residual(to_np(x[sl]), to_np(r[sl]), to_np(w), dtype=name)
         np.testing.assert_array_equal(to_np(s[sl]), es)
         assert_oracle(ey, to_np(y[sl]), dtype)
+        assert_oracle(oracle.rmsnorm(to_np(x[sl]), to_np(w), dtype=name), to_np(p[sl]), dtype)
 
 
 @pytest.mark.parametrize("cap", [1, 3, 7, 64])
