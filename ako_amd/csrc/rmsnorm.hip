@@ -638,10 +638,10 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
     if (order == 1) xcd_chunk = 1;
     if (order == 2) xcd_chunk = chunk > 0 ? unsigned(chunk) : unsigned(grid.x / 8);
     AKO_LAUNCH((rmsnorm_reg<T, W, WPR, VPT, RPB, RES, EW, SPLIT, WT>),
-                       grid, block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
-                       static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
-                       b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
-                       1.0f / static_cast<float>(a.hidden), a.eps, make_xcd_runs(xcd_chunk));
+               grid, block, lds, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+               static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout),
+               b0 * RPB, a.rows, static_cast<int>(a.hidden), a.sx, a.sr, a.sy, a.srout,
+               1.0f / static_cast<float>(a.hidden), a.eps, make_xcd_runs(xcd_chunk));
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -750,9 +750,9 @@ hipError_t run_pipe(const RmsArgs& a, hipStream_t stream) {
   const int64_t blocks = pipe_blocks(WPR, RES, a.rows);
   const int xcd_runs = g_rms_tuning.row_order == 1 ? 0 : 1;
   AKO_LAUNCH((rmsnorm_pipe<T, W, WPR, VPT, RES>), dim3(static_cast<unsigned>(blocks)), dim3(kWave * WPR),
-                     0, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
-                     static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout), a.rows, a.sx,
-                     a.sr, a.sy, a.srout, 1.0f / static_cast<float>(a.hidden), a.eps, xcd_runs);
+             0, stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+             static_cast<const W*>(a.w), static_cast<T*>(a.y), static_cast<T*>(a.rout), a.rows, a.sx,
+             a.sr, a.sy, a.srout, 1.0f / static_cast<float>(a.hidden), a.eps, xcd_runs);
   return hipGetLastError();
 }
 
@@ -812,10 +812,10 @@ hipError_t run_stream(const RmsArgs& a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
     if (a.vector_ok) {
       AKO_LAUNCH((rmsnorm_stream<T, W, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
-                         stream, x, r, w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+                 stream, x, r, w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
     } else {
       AKO_LAUNCH((rmsnorm_stream<T, W, 1, RES>), grid, dim3(kStreamBlock), 0, stream, x, r,
-                         w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
+                 w, y, ro, r0, h, a.sx, a.sr, a.sy, a.srout, inv_h, a.eps);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -872,14 +872,14 @@ hipError_t run_shard_partial(const RmsShardArgs& a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(std::min(cap, a.rows - r0)));
     if (a.vector_ok) {
       AKO_LAUNCH((rmsnorm_shard_partial<T, 16 / sizeof(T), RES>), grid, dim3(kStreamBlock), 0,
-                         stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
-                         static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
-                         a.sr, a.srout);
+                 stream, static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                 static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
+                 a.sr, a.srout);
     } else {
       AKO_LAUNCH((rmsnorm_shard_partial<T, 1, RES>), grid, dim3(kStreamBlock), 0, stream,
-                         static_cast<const T*>(a.x), static_cast<const T*>(a.r),
-                         static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
-                         a.sr, a.srout);
+                 static_cast<const T*>(a.x), static_cast<const T*>(a.r),
+                 static_cast<T*>(a.rout), a.partial, r0, static_cast<int>(a.shard), a.sx,
+                 a.sr, a.srout);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -896,14 +896,14 @@ hipError_t run_shard_apply_r(const RmsShardArgs& a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(ceil_div(end - r0, R)));
     if (a.vector_ok) {
       AKO_LAUNCH((rmsnorm_shard_apply<T, W, 16 / sizeof(T), R>), grid, dim3(kStreamBlock), 0,
-                         stream, static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
-                         static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
-                         a.eps);
+                 stream, static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
+                 static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                 a.eps);
     } else {
       AKO_LAUNCH((rmsnorm_shard_apply<T, W, 1, R>), grid, dim3(kStreamBlock), 0, stream,
-                         static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
-                         static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
-                         a.eps);
+                 static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.total,
+                 static_cast<T*>(a.y), r0, end, static_cast<int>(a.shard), a.sx, a.sy, inv_h,
+                 a.eps);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

@@ -310,7 +310,7 @@ hipError_t run_vec(RopeDev d, int64_t per_unit, hipStream_t stream) {
     else if (one_tensor && grid.x >= kRunsMinBlocks) chunk = kRun;
     part.runs = make_xcd_runs(chunk);
     AKO_LAUNCH((rope_vec<T, TT, NEOX, ITERS, TPB, CACHE>), grid, dim3(kWave * TPB), 0,
-                       stream, part);
+               stream, part);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

@@ -139,8 +139,8 @@ hipError_t run_flat(const SwigluArgs& a, hipStream_t stream) {
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
     const int64_t nb = std::min(kMaxBlocksPerLaunch, blocks - b0);
     AKO_LAUNCH((swiglu_flat<T, U, kBlock>), dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0,
-                       stream, static_cast<const T*>(a.g), static_cast<const T*>(a.u),
-                       static_cast<T*>(a.y), b0 * per_block, npk, nelems, runs);
+               stream, static_cast<const T*>(a.g), static_cast<const T*>(a.u),
+               static_cast<T*>(a.y), b0 * per_block, npk, nelems, runs);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -155,9 +155,9 @@ hipError_t run_rows(const SwigluArgs& a, hipStream_t stream) {
   for (int64_t r0 = 0; r0 < a.rows; r0 += rows_per_launch) {
     const int64_t nr = std::min(rows_per_launch, a.rows - r0);
     AKO_LAUNCH((swiglu_rows<T, E, U, kBlock>), dim3(static_cast<unsigned>(nr * tiles)),
-                       dim3(kBlock), 0, stream, static_cast<const T*>(a.g),
-                       static_cast<const T*>(a.u), static_cast<T*>(a.y), r0, n, tiles, a.sg, a.su,
-                       a.sy);
+               dim3(kBlock), 0, stream, static_cast<const T*>(a.g),
+               static_cast<const T*>(a.u), static_cast<T*>(a.y), r0, n, tiles, a.sg, a.su,
+               a.sy);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
