@@ -224,7 +224,9 @@ int ako_set_tuning(int op, int key, int value);
  * without the marker packets that an hipEventRecord on each side would queue
  * around it. The events are the caller's (hipEventCreate, timing enabled);
  * an entry point that makes several launches (inputs past 2^31 work-items)
- * times its first. Arming replaces a pair that no launch has taken.
+ * times its first. Arming replaces a pair that no launch has taken. Do
+ * not arm a pair while the thread captures a stream into a graph: the next
+ * launch takes it whether or not it is captured.
  * start and stop both NULL disarms: the return value is then 1 when a pair
  * was still armed (no launch took it), else AKO_OK. Exactly one NULL is
  * AKO_ERR_INVALID_ARGUMENT.
