@@ -76,7 +76,7 @@ struct RopeTuning {
 };
 struct SwigluTuning {
   TuningKey vecs_per_thread{0};  // key 1: packets per lane (1, 2, 4 or 8)
-  TuningKey xcd_chunk{0};        // key 2: consecutive workgroups per XCD run in dense launches (0 or 1 = block order)
+  TuningKey xcd_chunk{0};        // key 2: consecutive workgroups per XCD run in dense launches (1 = block order; 0 = runs of 4 for launches of 2048-65535 workgroups)
 };
 extern RmsTuning g_rms_tuning;
 extern RopeTuning g_rope_tuning;

@@ -128,16 +128,23 @@ hipError_t run_flat(const SwigluArgs& a, hipStream_t stream) {
   const int64_t npk = nelems / E;
   const int64_t per_block = int64_t(kBlock) * U;
   const int64_t blocks = std::max<int64_t>(1, ceil_div(npk, per_block));
-  // Workgroups go to the XCDs in block order unless key 2 asks for runs.
-  // Runs of 4 read +1.2 / +2.0 points of peak at M = 16384 / 4096 (bf16 x
-  // 14336) in one placement of the buffers, but over six placements (random
-  // spacers between the input copies, interleaved timings on MI355X) they
-  // averaged -0.2 points at M = 16384 (-0.8 to +0.1) and +0.7 at M = 4096
-  // (+0.3 to +1.5): not enough to change the default.
+  // Launches of kRunsMinBlocks to kRunsMaxBlocks - 1 workgroups hand them to
+  // the XCDs in runs of kRun; smaller ones (decode) and larger ones keep
+  // block order. Against block order, bf16 x 14336, 4-6 buffer placements
+  // (random spacers between the input copies, interleaved back-to-back
+  // timings) on each of five MI355X boxes: M = 4096 +0.7 to +2.5 points of
+  // peak (box means), M = 512-1024 +0.3 to +1.2, M = 8192 +1.25 (one box);
+  // M = 16384 (114688 workgroups) -0.55 to +0.9 by box, +0.2 on average;
+  // M = 256 (1792 workgroups) -0.3. Key 2 overrides (1 = block order).
+  constexpr int64_t kRunsMinBlocks = 2048;
+  constexpr int64_t kRunsMaxBlocks = 65536;
+  constexpr unsigned kRun = 4;
   const int forced = g_swiglu_tuning.xcd_chunk;
-  const XcdRuns runs = make_xcd_runs(forced > 1 ? static_cast<unsigned>(forced) : 1u);
   for (int64_t b0 = 0; b0 < blocks; b0 += kMaxBlocksPerLaunch) {
     const int64_t nb = std::min(kMaxBlocksPerLaunch, blocks - b0);
+    const bool runs_by_default = nb >= kRunsMinBlocks && nb < kRunsMaxBlocks;
+    const unsigned chunk = forced > 0 ? static_cast<unsigned>(forced) : (runs_by_default ? kRun : 1u);
+    const XcdRuns runs = make_xcd_runs(chunk);
     AKO_LAUNCH((swiglu_flat<T, U, kBlock>), dim3(static_cast<unsigned>(nb)), dim3(kBlock), 0,
                stream, static_cast<const T*>(a.g), static_cast<const T*>(a.u),
                static_cast<T*>(a.y), b0 * per_block, npk, nelems, runs);

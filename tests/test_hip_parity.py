@@ -733,16 +733,18 @@ def test_swiglu_config4(m: int) -> None:
                   torch.bfloat16)
 
 
-def test_swiglu_xcd_runs_cover_every_packet() -> None:
-    """Dense SwiGLU with workgroups handed to the XCDs in runs (key 2): the
-    map is a bijection on the grid, so every run length, including ones that
-    leave a partial last round and trailing workgroups, gives the
-    block-order output bit for bit, and the tail elements past the last full
-    packet are still written."""
+@pytest.mark.parametrize("rows", [77, 300])
+def test_swiglu_xcd_runs_cover_every_packet(rows: int) -> None:
+    """Dense SwiGLU with workgroups handed to the XCDs in runs (key 2; by
+    default runs of 4 for launches of 2048-65535 workgroups, which 300 rows
+    of 14343 reach with 2101 and 77 rows do not): the map is a bijection on
+    the grid, so every run length, including ones that leave a partial last
+    round and trailing workgroups, gives the block-order output bit for bit,
+    and the tail elements past the last full packet are still written."""
     from ako_amd import _native
 
-    g = grandn((77, 14343), torch.bfloat16, 17, scale=4.0)
-    u = grandn((77, 14343), torch.bfloat16, 18)
+    g = grandn((rows, 14343), torch.bfloat16, 17, scale=4.0)
+    u = grandn((rows, 14343), torch.bfloat16, 18)
     try:
         _native.set_tuning(2, 2, 1)
         want = swiglu_hip(g, u)
