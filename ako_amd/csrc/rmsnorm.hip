@@ -580,17 +580,22 @@ RegShape pick_shape(int64_t nvec, bool residual, int64_t rows) {
 }
 
 constexpr unsigned kXcdChunk = 8;
-// Rows of 16384 half elements (the (16, 2) shape, write-through stores;
-// residual rows one workgroup per CU with one packet per load group) take
-// runs of 4. Buffer placements (random spacer allocations between the input
-// copies), variants interleaved, medians of settled back-to-back runs on
-// MI355X. Plain rows, five placements on each of three boxes, against runs
-// of 8: fp16 +0.29 to +0.30 points of peak (per placement -0.06 to +0.71),
-// bf16 +0.56 to +0.70 (+0.20 to +0.97); runs of 16 -0.23 to -0.29. Residual
-// rows, four placements on each of three boxes, against runs of 16 (which
-// beat runs of 8 by 0.3-0.6): fp16 +0.29 to +0.34, bf16 +0.10 to +0.15
-// (per placement -0.5 to +1.0).
-constexpr unsigned kXcdChunkWide = 4;
+// Residual rows of 16384 half elements (the one-workgroup-per-CU launches
+// below, write-through stores, one packet per load group) take runs of 16.
+// Medians of 7-10 rotating back-to-back runs on MI355X, same buffers, outputs
+// identical, three boxes: runs of 16 gained 0.4-1.4 points of peak over runs
+// of 8 (e.g. 81.5% / 82.7% against 80.3% / 81.3%, bf16 / fp16); runs of 12,
+// 20, 24 and 32 were no better than 8, and the whole 12-launch step read
+// 6542 against 6525 GB/s. Plain rows of 16384 and residual rows of 8192
+// showed no consistent gain from 16.
+constexpr unsigned kXcdChunkWideResidual = 16;
+// Plain rows of 16384 half elements take runs of 4. Five buffer placements
+// (random spacer allocations between the input copies) on each of three
+// MI355X boxes, variants interleaved, medians of settled back-to-back runs:
+// against runs of 8, fp16 +0.29 to +0.30 points of peak (per-placement
+// -0.06 to +0.71), bf16 +0.56 to +0.70 (+0.20 to +0.97); runs of 16 were
+// -0.23 to -0.29.
+constexpr unsigned kXcdChunkWidePlain = 4;
 
 // Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
 // the dispatch packet never wraps; larger problems take several launches,
@@ -617,10 +622,10 @@ hipError_t run_reg_launch(const RmsArgs& a, hipStream_t stream) {
   unsigned lds = static_cast<unsigned>(g_rms_tuning.lds_reserve);
   if (lds == 0 && one_per_cu) lds = 82 * 1024;
   unsigned run = kXcdChunk;
-  if (WPR == 16 && VPT == 2 && sizeof(T) == 2 && row32k) run = kXcdChunkWide;
+  if (WPR == 16 && VPT == 2 && sizeof(T) == 2 && row32k) run = RES ? kXcdChunkWideResidual : kXcdChunkWidePlain;
   // Default: rows of >= 16 KiB go to the XCDs in runs of 8 consecutive rows
-  // (4 for rows of 16384 half elements; once the launch holds 8 such runs);
-  // narrower rows keep block order.
+  // (rows of 16384 half elements: 16 residual, 4 plain; once the launch
+  // holds 8 such runs); narrower rows keep block order.
   // Medians of 5 cold runs on MI355X, 16384 rows, fp16/bf16, against block
   // order: +1% at 16 KiB rows, +4% (plain) and +8-10% (residual) at 32 KiB
   // rows, -1-2% at 8 KiB rows; whole-grid runs (chunk = n / 8) lose up to 12%

@@ -213,8 +213,9 @@ def test_rmsnorm_xcd_row_orders_cover_every_row(rows: int) -> None:
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows", [31, 33, 127, 130, 257, 1000, 2051])
 def test_rmsnorm_wide_rows_xcd_runs_cover_every_row(rows: int, dtype: torch.dtype) -> None:
-    """Rows of 16384 half elements go to the XCDs in runs of 4 from 32
-    workgroups up (block order below), residual and plain rows alike. Row
+    """Rows of 16384 half elements go to the XCDs in runs: residual rows in
+    runs of 16 from 128 workgroups up (runs of 8 from 64, block order below),
+    plain rows in runs of 4 from 32 workgroups up (block order below). Row
     counts straddle those thresholds and the 256-row switch to write-through
     stores, and 1000 / 2051 leave partial runs and trailing blocks; the
     default order must give bit-identical outputs to block order, which is
