@@ -587,14 +587,19 @@ constexpr unsigned kXcdChunk = 8;
 // of 8 (e.g. 81.5% / 82.7% against 80.3% / 81.3%, bf16 / fp16); runs of 12,
 // 20, 24 and 32 were no better than 8, and the whole 12-launch step read
 // 6542 against 6525 GB/s. Plain rows of 16384 and residual rows of 8192
-// showed no consistent gain from 16.
+// showed no consistent gain from 16. Runs of 4 read +0.1 to +0.3 over 16
+// with random spacer allocations between the inputs (four placements on
+// each of four boxes), but -0.9 (bf16) and -0.1 (fp16) with the inputs
+// allocated back to back, five repetitions on each of two boxes, so 16
+// stays.
 constexpr unsigned kXcdChunkWideResidual = 16;
 // Plain rows of 16384 half elements take runs of 4. Five buffer placements
 // (random spacer allocations between the input copies) on each of three
 // MI355X boxes, variants interleaved, medians of settled back-to-back runs:
 // against runs of 8, fp16 +0.29 to +0.30 points of peak (per-placement
 // -0.06 to +0.71), bf16 +0.56 to +0.70 (+0.20 to +0.97); runs of 16 were
-// -0.23 to -0.29.
+// -0.23 to -0.29. With the inputs allocated back to back: bf16 +0.7 to
+// +0.9 over runs of 8 on two boxes.
 constexpr unsigned kXcdChunkWidePlain = 4;
 
 // Workgroups per launch: at most 2^31 work-items, so the 32-bit grid size of
