@@ -49,22 +49,37 @@ def parse_cell(name: str) -> dict[str, Any]:
 
 def _b2b_pct(row: dict[str, Any]) -> float:
     """A row's share of peak timed back to back: the step's cells carry it
-    under ``back_to_back`` (their top-level figure has an event pair around
-    each launch, which costs 1.5-2 us per launch); the extras are timed back
-    to back already."""
+    under ``back_to_back`` (their top-level figure is per launch); the extras
+    are timed back to back at the top level."""
     return (row.get("back_to_back") or {}).get("pct_hbm_peak", row["pct_hbm_peak"])
+
+
+def _launch_pct(row: dict[str, Any]) -> float | None:
+    """A row's share of peak per launch, from events bound to each launch
+    (the kernel's own duration): the step's cells at the top level, the
+    extras under ``per_launch`` (None when they have none)."""
+    if "back_to_back" in row:
+        return row["pct_hbm_peak"]
+    return (row.get("per_launch") or {}).get("pct_hbm_peak")
 
 
 def prefill_floor(rows: list[dict[str, Any]]) -> dict[str, dict[str, Any]]:
     """Per op, the prefill cell with the lowest share of peak timed back to
-    back (and how many prefill cells there were), from rows carrying
-    ``name``/``pct_hbm_peak`` (and ``back_to_back`` for the step's cells)."""
+    back (and how many prefill cells there were), and the lowest per-launch
+    figure where the cells have one, from rows carrying ``name``/
+    ``pct_hbm_peak`` (``back_to_back`` for the step's cells, ``per_launch``
+    for the extras)."""
     out: dict[str, dict[str, Any]] = {}
     for op, pat in PREFILL.items():
         hits = [r for r in rows if pat.match(r["name"])]
         if hits:
             low = min(hits, key=_b2b_pct)
             out[op] = {"min_pct": _b2b_pct(low), "cell": low["name"], "cells": len(hits)}
+            timed = [(p, r["name"]) for r in hits if (p := _launch_pct(r)) is not None]
+            if len(timed) == len(hits):
+                pct, name = min(timed)
+                out[op]["min_per_launch_pct"] = pct
+                out[op]["per_launch_cell"] = name
     return out
 
 

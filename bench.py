@@ -33,9 +33,10 @@ The printed line (one JSON object, kept under 8 KB) also carries:
                 with decode steps replayed from a HIP graph;
   rope_prefill  RoPE at (4, 2048) as the fused q+k launch, and as the
                 decoder's own prefill call, which also writes k and v into
-                its KV cache (qk_cache);
+                its KV cache (qk_cache); back to back, and per launch with
+                launch-bound events (per_launch: the kernel's own duration);
   prefill_floor per op, the prefill cell with the lowest share of peak,
-                timed back to back.
+                timed back to back, and the lowest per launch.
 
 Every timed cell goes to ``--cells-out`` (reports/mi355x/bench_cells.json by
 default) in the reference's report layout, with the selection's rows:
@@ -45,9 +46,11 @@ default) in the reference's report layout, with the selection's rows:
                 input copies, beside a copy timed the same way;
   extras        the RoPE and SwiGLU cells, the
                 decode-size RMSNorm cells, the KV-cache RoPE and the
-                tensor-parallel RMSNorm halves; streaming cells beside their
-                copy ceiling, decode cells as graph-replayed device time with
-                inputs hot (graph_us) and in no cache (graph_cold_us).
+                tensor-parallel RMSNorm halves; streaming cells back to back
+                and per launch (launch-bound events over three passes of
+                their cold input copies), each beside the copy timed the same
+                way, decode cells as graph-replayed device time with inputs
+                hot (graph_us) and in no cache (graph_cold_us).
 
 ``dtype`` is the arithmetic type of the kernels (fp32); the stored tensors
 are fp16 and bf16 (``config.storage_dtypes``).
@@ -295,6 +298,26 @@ def extras_cells(torch, rf, dev, rnd):
     return cells
 
 
+def per_launch_row(name, nbytes, fns, rf, peak, ceilings) -> dict | None:
+    """A streaming cell's launches timed one by one with events bound to each
+    launch (the kernel's own duration, as the roofline is timed), three
+    passes over its cold input copies, beside the copy's per-launch figure.
+    None when a call makes no launch through the library."""
+    calls = [(name, nbytes, fn) for fn in fns]
+    try:
+        stats = rf.time_each_launch(calls, steps=3, lead_passes=1, kernel_events=True)[0]
+    except RuntimeError as err:
+        log(f"{name}: no launch-bound timing ({err})")
+        return None
+    out = {"mean_us": round(stats.mean_ms * 1e3, 3), "launches": len(stats.durations_ms),
+           "pct_hbm_peak": round(100.0 * stats.gbps() / peak, 2)}
+    copy = ceilings.get(nbytes)
+    if copy is not None:
+        out["copy_pct_hbm_peak"] = round(100 * copy["frac"], 2)
+        out["kernel_over_copy"] = round(stats.gbps() / copy["gbps"], 4)
+    return out
+
+
 def time_extras(cells, torch, rf, peak, ceilings):
     """Each cell: 60 back-to-back launches over its input copies between one
     event pair (per-launch events would distort 5-30 us kernels; streaming
@@ -321,6 +344,7 @@ def time_extras(cells, torch, rf, peak, ceilings):
         row["copies"] = 1 if decode else len(fns)
         if nbytes >= STREAMING_BYTES:
             ceilings.annotate(row, stats.gbps(), back_to_back=True)
+            row["per_launch"] = per_launch_row(name, nbytes, fns, rf, peak, ceilings)
         if decode:
             # Median of five graph timings: one is under a millisecond of
             # device time, and clock changes move single readings by up to 15%.
@@ -415,6 +439,13 @@ def in_model_decode(torch, rf, dev, rnd):
             "calls_per_step": sum(DECODE_STEP_CALLS.values())}
 
 
+def _per_launch_brief(row: dict) -> dict | None:
+    per = row.get("per_launch")
+    if not per:
+        return None
+    return {k: per[k] for k in ("pct_hbm_peak", "kernel_over_copy") if k in per}
+
+
 def rope_prefill_summary(extras, ceilings):
     """RoPE at the prefill shape: q and k in one launch (configs[2]'s pair),
     and the decoder's own call, which also writes k and v into the KV cache."""
@@ -427,11 +458,13 @@ def rope_prefill_summary(extras, ceilings):
         if qk is None:
             continue
         out[tag] = {"cell": qk["name"], "pct_hbm_peak": qk["pct_hbm_peak"],
-                    "copy_pct_hbm_peak": qk.get("copy_pct_hbm_peak"), "kernel_over_copy": qk.get("kernel_over_copy")}
+                    "copy_pct_hbm_peak": qk.get("copy_pct_hbm_peak"), "kernel_over_copy": qk.get("kernel_over_copy"),
+                    "per_launch": _per_launch_brief(qk)}
         if cache is not None:
             out[tag]["qk_cache"] = {"pct_hbm_peak": cache["pct_hbm_peak"],
                                     "copy_pct_hbm_peak": cache.get("copy_pct_hbm_peak"),
-                                    "kernel_over_copy": cache.get("kernel_over_copy")}
+                                    "kernel_over_copy": cache.get("kernel_over_copy"),
+                                    "per_launch": _per_launch_brief(cache)}
         if k is not None:
             out[tag]["k_alone"] = {"pct_hbm_peak": k["pct_hbm_peak"], "copy_pct_hbm_peak": k.get("copy_pct_hbm_peak"),
                                    "note": "34 MB launch: a copy of that size reaches little more"}
